@@ -1,0 +1,454 @@
+// C-ABI layer of libasmllm.so: argument checks, host/device pointer staging for
+// the reference-named synchronous entry points, and the device plumbing calls.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "asmllm_hip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace asmhip {
+
+namespace {
+thread_local char g_last_error[1024] = "";
+
+constexpr int kMaxDevices = 64;
+constexpr int kMaxPool = 64;  // threadpool.c:99 MAX_WORKERS
+
+// Per-device library state used by the synchronous entry points: one stream
+// (default priority) and a grow-only staging buffer for host operands.
+struct DeviceState {
+    hipStream_t stream = nullptr;
+    void* staging = nullptr;
+    size_t staging_bytes = 0;
+};
+
+std::mutex g_mu;
+DeviceState g_dev[kMaxDevices];
+int g_pool_size = 0;  // what asm_threadpool_init recorded
+}  // namespace
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(kHipError, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+namespace {
+
+int current_device(int* dev) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return fail(kNoDevice, "no HIP device available");
+    }
+    ASMHIP_TRY(hipGetDevice(dev));
+    if (*dev < 0 || *dev >= kMaxDevices) return fail(kUnsupported, "device index %d out of range", *dev);
+    return kOk;
+}
+
+// Caller holds g_mu.
+int ensure_state(DeviceState** out) {
+    int dev = 0;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    DeviceState& st = g_dev[dev];
+    if (!st.stream) ASMHIP_TRY(hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking));
+    *out = &st;
+    return kOk;
+}
+
+int ensure_staging(DeviceState* st, size_t bytes) {
+    if (st->staging_bytes >= bytes) return kOk;
+    if (st->staging) {
+        ASMHIP_TRY(hipStreamSynchronize(st->stream));
+        ASMHIP_TRY(hipFree(st->staging));
+        st->staging = nullptr;
+        st->staging_bytes = 0;
+    }
+    size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    ASMHIP_TRY(hipMalloc(&st->staging, want));
+    st->staging_bytes = want;
+    return kOk;
+}
+
+bool is_device_pointer(const void* p) {
+    if (!p) return false;
+    hipPointerAttribute_t a;
+    hipError_t e = hipPointerGetAttributes(&a, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged;
+}
+
+// One operand of a synchronous call: where it lives and where the kernel reads it.
+struct Operand {
+    const void* host;  // user pointer
+    size_t bytes;
+    bool on_device;
+    void* dev;  // device address used by the kernel
+};
+
+size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Places every host operand in the staging buffer and uploads the inputs.
+int stage(DeviceState* st, Operand* ops, int n_ops, int n_inputs) {
+    size_t need = 0;
+    for (int i = 0; i < n_ops; ++i) {
+        ops[i].on_device = is_device_pointer(ops[i].host);
+        if (!ops[i].on_device) need += round256(ops[i].bytes);
+    }
+    if (need) {
+        int rc = ensure_staging(st, need);
+        if (rc) return rc;
+    }
+    size_t off = 0;
+    for (int i = 0; i < n_ops; ++i) {
+        if (ops[i].on_device) {
+            ops[i].dev = const_cast<void*>(ops[i].host);
+            continue;
+        }
+        ops[i].dev = static_cast<char*>(st->staging) + off;
+        off += round256(ops[i].bytes);
+        if (i < n_inputs)
+            ASMHIP_TRY(hipMemcpyAsync(ops[i].dev, ops[i].host, ops[i].bytes, hipMemcpyHostToDevice, st->stream));
+    }
+    return kOk;
+}
+
+// Downloads host-resident outputs (ops[first..n_ops)) and waits for the stream.
+int finish(DeviceState* st, Operand* ops, int n_ops, int first_output) {
+    for (int i = first_output; i < n_ops; ++i)
+        if (!ops[i].on_device)
+            ASMHIP_TRY(hipMemcpyAsync(const_cast<void*>(ops[i].host), ops[i].dev, ops[i].bytes,
+                                      hipMemcpyDeviceToHost, st->stream));
+    ASMHIP_TRY(hipStreamSynchronize(st->stream));
+    return kOk;
+}
+
+void report(int rc, const char* fn) {
+    if (rc != kOk) fprintf(stderr, "[libasmllm] %s: %s\n", fn, g_last_error);
+}
+
+int sync_matvec(QuantType qt, const void* q, const float* s, const float* x, float* y, int64_t M, int64_t K) {
+    if (!q || !s || !x || !y) return fail(kInvalidArgument, "null pointer argument");
+    if (M <= 0 || K <= 0 || K % 32 != 0)
+        return fail(kInvalidArgument, "need M > 0, K > 0 and K %% 32 == 0 (got M=%lld K=%lld)", (long long)M,
+                    (long long)K);
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState* st = nullptr;
+    int rc = ensure_state(&st);
+    if (rc) return rc;
+    const size_t nb = (size_t)(K / 32);
+    Operand ops[4] = {
+        {q, (size_t)M * nb * (qt == QuantType::Q4_0 ? 16 : 32), false, nullptr},
+        {s, (size_t)M * nb * sizeof(float), false, nullptr},
+        {x, (size_t)K * sizeof(float), false, nullptr},
+        {y, (size_t)M * sizeof(float), false, nullptr},
+    };
+    rc = stage(st, ops, 4, 3);
+    if (rc) return rc;
+    rc = matvec_launch(qt, false, ops[0].dev, static_cast<const float*>(ops[1].dev),
+                       static_cast<const float*>(ops[2].dev), static_cast<float*>(ops[3].dev), M, K, st->stream);
+    if (rc) {
+        (void)hipStreamSynchronize(st->stream);
+        return rc;
+    }
+    return finish(st, ops, 4, 3);
+}
+
+void record_pool_size(int n) {
+    if (n < 1) n = 1;
+    if (n > kMaxPool) n = kMaxPool;
+    g_pool_size = n;
+}
+
+}  // namespace
+}  // namespace asmhip
+
+using namespace asmhip;
+
+// ---- reference-named entry points -------------------------------------------
+
+extern "C" void asm_matmul_q4(const uint8_t* qweights, const float* scales, const float* x, float* y, int64_t M,
+                              int64_t K) {
+    report(sync_matvec(QuantType::Q4_0, qweights, scales, x, y, M, K), "asm_matmul_q4");
+}
+
+extern "C" void asm_matmul_q4_avx512(const uint8_t* qweights, const float* scales, const float* x, float* y,
+                                     int64_t M, int64_t K) {
+    report(sync_matvec(QuantType::Q4_0, qweights, scales, x, y, M, K), "asm_matmul_q4_avx512");
+}
+
+extern "C" void asm_matmul_q8(const int8_t* qweights, const float* scales, const float* x, float* y, int64_t M,
+                              int64_t K) {
+    report(sync_matvec(QuantType::Q8_0, qweights, scales, x, y, M, K), "asm_matmul_q8");
+}
+
+extern "C" void asm_threadpool_init(int num_threads) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState* st = nullptr;
+    int rc = ensure_state(&st);
+    if (rc) {
+        report(rc, "asm_threadpool_init");
+        return;
+    }
+    record_pool_size(num_threads);
+}
+
+extern "C" void asm_threadpool_shutdown(void) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (g_pool_size <= 0) return;  // threadpool.c:372
+    int dev = 0;
+    if (current_device(&dev) == kOk) {
+        DeviceState& st = g_dev[dev];
+        if (st.stream) {
+            (void)hipStreamSynchronize(st.stream);
+            (void)hipStreamDestroy(st.stream);
+            st.stream = nullptr;
+        }
+        if (st.staging) {
+            (void)hipFree(st.staging);
+            st.staging = nullptr;
+            st.staging_bytes = 0;
+        }
+    }
+    g_pool_size = 0;
+}
+
+extern "C" int asm_threadpool_get_num_threads(void) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    return g_pool_size;
+}
+
+// threadpool.c:399-406: below 32 rows or one thread the pool is not touched;
+// otherwise the pool is (re)sized to num_threads.
+static void mt_pool_update(int64_t M, int num_threads) {
+    if (num_threads <= 1 || M < 32) return;
+    bool resize;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        resize = g_pool_size != num_threads;
+    }
+    if (resize) asm_threadpool_init(num_threads);
+}
+
+extern "C" void asm_matmul_q4_mt(const uint8_t* qweights, const float* scales, const float* x, float* y,
+                                 int64_t M, int64_t K, int num_threads) {
+    mt_pool_update(M, num_threads);
+    report(sync_matvec(QuantType::Q4_0, qweights, scales, x, y, M, K), "asm_matmul_q4_mt");
+}
+
+extern "C" void asm_matmul_q8_mt(const int8_t* qweights, const float* scales, const float* x, float* y,
+                                 int64_t M, int64_t K, int num_threads) {
+    mt_pool_update(M, num_threads);
+    report(sync_matvec(QuantType::Q8_0, qweights, scales, x, y, M, K), "asm_matmul_q8_mt");
+}
+
+extern "C" void asm_threadpool_dispatch_q8(const int8_t* qweights, const float* scales, const float* x, float* y,
+                                           int64_t M, int64_t K) {
+    report(sync_matvec(QuantType::Q8_0, qweights, scales, x, y, M, K), "asm_threadpool_dispatch_q8");
+}
+
+// ---- device entry points -------------------------------------------------------
+
+static int check_ptrs(const void* a, const void* b, const void* c) {
+    if (!a || !b || !c) return fail(kInvalidArgument, "null pointer argument");
+    return kOk;
+}
+
+extern "C" int asmhip_matmul_q4_0(const void* blocks, const float* x, float* y, int64_t M, int64_t K, void* stream) {
+    int rc = check_ptrs(blocks, x, y);
+    return rc ? rc : matvec_launch(QuantType::Q4_0, true, blocks, nullptr, x, y, M, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_matmul_q8_0(const void* blocks, const float* x, float* y, int64_t M, int64_t K, void* stream) {
+    int rc = check_ptrs(blocks, x, y);
+    return rc ? rc : matvec_launch(QuantType::Q8_0, true, blocks, nullptr, x, y, M, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_matmul_q4_split(const uint8_t* qweights, const float* scales, const float* x, float* y,
+                                      int64_t M, int64_t K, void* stream) {
+    int rc = check_ptrs(qweights, x, y);
+    if (!rc && !scales) rc = fail(kInvalidArgument, "null scales");
+    return rc ? rc : matvec_launch(QuantType::Q4_0, false, qweights, scales, x, y, M, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_matmul_q8_split(const int8_t* qweights, const float* scales, const float* x, float* y,
+                                      int64_t M, int64_t K, void* stream) {
+    int rc = check_ptrs(qweights, x, y);
+    if (!rc && !scales) rc = fail(kInvalidArgument, "null scales");
+    return rc ? rc : matvec_launch(QuantType::Q8_0, false, qweights, scales, x, y, M, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_dequantize_q4_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream) {
+    if (!blocks || !w) return fail(kInvalidArgument, "null pointer argument");
+    return dequant_launch(QuantType::Q4_0, blocks, w, rows, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_dequantize_q8_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream) {
+    if (!blocks || !w) return fail(kInvalidArgument, "null pointer argument");
+    return dequant_launch(QuantType::Q8_0, blocks, w, rows, K, (hipStream_t)stream);
+}
+
+// ---- plumbing --------------------------------------------------------------------
+
+extern "C" int asmhip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+extern "C" int asmhip_device_info(char* name, size_t name_len, int* compute_units, int* clock_khz,
+                                  size_t* total_mem) {
+    int dev = 0;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    hipDeviceProp_t p;
+    ASMHIP_TRY(hipGetDeviceProperties(&p, dev));
+    if (name && name_len) {
+        snprintf(name, name_len, "%s", p.gcnArchName);
+    }
+    if (compute_units) *compute_units = p.multiProcessorCount;
+    if (clock_khz) *clock_khz = p.clockRate;
+    if (total_mem) *total_mem = p.totalGlobalMem;
+    return kOk;
+}
+
+extern "C" void* asmhip_malloc(size_t bytes) {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipMalloc");
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
+
+extern "C" int asmhip_free(void* ptr) {
+    if (!ptr) return kOk;
+    ASMHIP_TRY(hipFree(ptr));
+    return kOk;
+}
+
+extern "C" int asmhip_memcpy(void* dst, const void* src, size_t bytes, int kind) {
+    hipMemcpyKind k;
+    switch (kind) {
+        case 1: k = hipMemcpyHostToDevice; break;
+        case 2: k = hipMemcpyDeviceToHost; break;
+        case 3: k = hipMemcpyDeviceToDevice; break;
+        default: return fail(kInvalidArgument, "memcpy kind %d (use 1 h2d, 2 d2h, 3 d2d)", kind);
+    }
+    if (!bytes) return kOk;
+    if (!dst || !src) return fail(kInvalidArgument, "null pointer argument");
+    ASMHIP_TRY(hipMemcpy(dst, src, bytes, k));
+    return kOk;
+}
+
+extern "C" int asmhip_synchronize(void) {
+    ASMHIP_TRY(hipDeviceSynchronize());
+    return kOk;
+}
+
+extern "C" void* asmhip_stream_create(void) {
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipStreamCreateWithFlags");
+        return nullptr;
+    }
+    return (void*)s;
+}
+
+extern "C" int asmhip_stream_destroy(void* stream) {
+    if (!stream) return kOk;
+    ASMHIP_TRY(hipStreamDestroy((hipStream_t)stream));
+    return kOk;
+}
+
+extern "C" int asmhip_stream_synchronize(void* stream) {
+    ASMHIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return kOk;
+}
+
+extern "C" void* asmhip_event_create(void) {
+    hipEvent_t e = nullptr;
+    hipError_t r = hipEventCreate(&e);
+    if (r != hipSuccess) {
+        hip_fail(r, "hipEventCreate");
+        return nullptr;
+    }
+    return (void*)e;
+}
+
+extern "C" int asmhip_event_destroy(void* event) {
+    if (!event) return kOk;
+    ASMHIP_TRY(hipEventDestroy((hipEvent_t)event));
+    return kOk;
+}
+
+extern "C" int asmhip_event_record(void* event, void* stream) {
+    if (!event) return fail(kInvalidArgument, "null event");
+    ASMHIP_TRY(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+    return kOk;
+}
+
+extern "C" int asmhip_event_synchronize(void* event) {
+    if (!event) return fail(kInvalidArgument, "null event");
+    ASMHIP_TRY(hipEventSynchronize((hipEvent_t)event));
+    return kOk;
+}
+
+extern "C" int asmhip_event_elapsed_ms(void* start, void* stop, float* ms) {
+    if (!start || !stop || !ms) return fail(kInvalidArgument, "null argument");
+    ASMHIP_TRY(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return kOk;
+}
+
+extern "C" int asmhip_stream_begin_capture(void* stream) {
+    if (!stream) return fail(kInvalidArgument, "capture needs a created stream, not the default stream");
+    ASMHIP_TRY(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    return kOk;
+}
+
+extern "C" int asmhip_stream_end_capture(void* stream, void** graph_exec) {
+    if (!stream || !graph_exec) return fail(kInvalidArgument, "null argument");
+    hipGraph_t graph = nullptr;
+    ASMHIP_TRY(hipStreamEndCapture((hipStream_t)stream, &graph));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *graph_exec = (void*)exec;
+    return kOk;
+}
+
+extern "C" int asmhip_graph_launch(void* graph_exec, void* stream) {
+    if (!graph_exec) return fail(kInvalidArgument, "null graph");
+    ASMHIP_TRY(hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream));
+    return kOk;
+}
+
+extern "C" int asmhip_graph_destroy(void* graph_exec) {
+    if (!graph_exec) return kOk;
+    ASMHIP_TRY(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    return kOk;
+}
+
+extern "C" const char* asmhip_last_error(void) { return g_last_error; }

@@ -1,0 +1,494 @@
+// Q4_0 / Q8_0 matrix-vector kernels for gfx950.
+//
+// y[m] = sum_b d[m,b] * sum_j (q[m,b,j] - bias) * x[32b + j]
+//
+// Replaces the reference's asm_matmul_q4 (src/kernels/x86_64/matmul_q4_avx2.asm:57-287)
+// and asm_matmul_q8 (src/kernels/x86_64/matmul_q8_avx2.asm:51-194).  Two weight
+// layouts are read in place:
+//   * GGUF blocks: Q4_0 = fp16 d + 16 B of nibbles (18 B / 32 weights),
+//                  Q8_0 = fp16 d + 32 int8       (34 B / 32 weights);
+//   * the reference's split layout: qs[M][K/32][16 or 32] + fp32 scales[M][K/32].
+// Byte j of a Q4 block holds weight j in its low nibble and weight j+16 in its
+// high nibble (matmul_q4_avx2.asm:122-153, tests/reference/ops.py:24-28).
+//
+// Work mapping (one wave = 64 lanes):
+//   * a lane owns one PAIR of consecutive blocks (64 columns) of a 64-pair
+//     column chunk, so a wave's loads for one row cover a contiguous
+//     64 x 36 B (Q4_0 GGUF) span of HBM; pairs keep GGUF rows dword-aligned;
+//   * a wave walks R rows at a time through every chunk, the x values of its
+//     pair sit in registers and are reused for all R rows;
+//   * x is staged once per workgroup in LDS (padded 4 floats per 64 so the
+//     per-lane 256 B reads are bank-conflict free), together with the per-block
+//     sum of x, which turns sum (q - 8) x into sum q x - 8 sum x;
+//   * nibbles become floats with one v_cvt_f32_ubyte{k} each: low nibbles via
+//     v & 0x0F0F0F0F, high nibbles via v & 0xF0F0F0F0 (= 16 q) against x / 16,
+//     both exact;
+//   * each lane keeps one fp32 accumulator per row, reduced across the wave
+//     at the end.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace asmhip {
+
+namespace {
+
+constexpr int kThreads = 256;  // 4 waves per workgroup
+constexpr int kWavesPerBlock = kThreads / kWave;
+
+__device__ __forceinline__ int xpad(int i) { return i + ((i >> 6) << 2); }
+
+// Hide the masked word from the instruction combiner so that each byte is
+// converted by one v_cvt_f32_ubyte{k} instead of a bfe + cvt pair.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
+// Low/high nibbles of bytes [k0, k1) of v are weights jb.. and jb+16.. of a
+// Q4 block; xl holds x[j], xh holds x[16 + j] / 16.
+template <int k0, int k1, int jb>
+__device__ __forceinline__ float q4_bytes(uint32_t v, const float* xl, const float* xh, float t) {
+    const uint32_t lo = opaque(v & 0x0F0F0F0Fu);
+    const uint32_t hi = opaque(v & 0xF0F0F0F0u);
+#pragma unroll
+    for (int k = k0; k < k1; ++k) {
+        t = fmaf((float)((lo >> (8 * k)) & 0xFFu), xl[jb + k - k0], t);
+        t = fmaf((float)((hi >> (8 * k)) & 0xFFu), xh[jb + k - k0], t);
+    }
+    return t;
+}
+
+// Signed bytes [k0, k1) of v (biased by +128 through the xor) times x[jb..].
+template <int k0, int k1, int jb>
+__device__ __forceinline__ float q8_bytes(uint32_t v, const float* xv, float t) {
+    const uint32_t u = opaque(v ^ 0x80808080u);
+#pragma unroll
+    for (int k = k0; k < k1; ++k) t = fmaf((float)((u >> (8 * k)) & 0xFFu), xv[jb + k - k0], t);
+    return t;
+}
+
+// Stage x into LDS (padded layout) and the per-block bias terms.
+// For Q4 the upper half of each block is pre-scaled by 1/16 and bias[b] is
+// 8 * sum x_b; for Q8 x is stored as is and bias[b] is 128 * sum x_b.
+template <bool kQ4>
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, float* xs, float* bias, int K) {
+    for (int i = threadIdx.x; i < K; i += kThreads) {
+        float v = x[i];
+        if (kQ4 && (i & 16)) v *= 0.0625f;
+        xs[xpad(i)] = v;
+    }
+    __syncthreads();
+    const int nb = K >> 5;
+    for (int b = threadIdx.x; b < nb; b += kThreads) {
+        const float* xb = xs + xpad(b * 32);  // a block never straddles a 64-float pad group
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            s0 += xb[j];
+            s1 += xb[16 + j];
+        }
+        bias[b] = kQ4 ? 8.0f * (s0 + 16.0f * s1) : 128.0f * (s0 + s1);
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Q4_0 pair kernel.  kGguf: 18-byte blocks; otherwise split qs + fp32 scales.
+// ---------------------------------------------------------------------------
+template <int R, bool kGguf>
+__global__ __launch_bounds__(kThreads) void q4_matvec_pairs(const uint8_t* __restrict__ w,
+                                                            const float* __restrict__ wscale,
+                                                            const float* __restrict__ x,
+                                                            float* __restrict__ y, int M, int K) {
+    extern __shared__ float smem[];
+    float* xs = smem;
+    float* bias = smem + K + (K >> 4);
+    stage_x<true>(x, xs, bias, K);
+
+    const int nb = K >> 5;
+    const int np = nb >> 1;
+    const uint32_t row_bytes = kGguf ? (uint32_t)nb * 18u : (uint32_t)nb * 16u;
+    const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
+    const auto sr = make_rsrc(wscale, kGguf ? 0u : (uint32_t)nb * 4u * (uint32_t)M);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nwaves = gridDim.x * kWavesPerBlock;
+
+    for (int g = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6); g * R < M; g += nwaves) {
+        const int row0 = g * R;
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+
+        for (int c0 = 0; c0 < np; c0 += kWave) {
+            const int p = c0 + lane;
+            const bool active = p < np;
+            const int pc = active ? p : np - 1;
+
+            uint32_t v[R][9];
+            float dA[R], dB[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = min(row0 + r, M - 1);
+                if (kGguf) {
+                    const uint32_t off = (uint32_t)row * row_bytes + (uint32_t)pc * 36u;
+                    const uint4 a = buf_load_b128(wr, off);
+                    const uint4 b = buf_load_b128(wr, off + 16u);
+                    v[r][0] = a.x; v[r][1] = a.y; v[r][2] = a.z; v[r][3] = a.w;
+                    v[r][4] = b.x; v[r][5] = b.y; v[r][6] = b.z; v[r][7] = b.w;
+                    v[r][8] = buf_load_b32(wr, off + 32u);
+                } else {
+                    const uint32_t blk = (uint32_t)row * (uint32_t)nb + 2u * (uint32_t)pc;
+                    const uint4 a = buf_load_b128(wr, blk * 16u);
+                    const uint4 b = buf_load_b128(wr, blk * 16u + 16u);
+                    const uint2 s = buf_load_b64(sr, blk * 4u);
+                    v[r][0] = a.x; v[r][1] = a.y; v[r][2] = a.z; v[r][3] = a.w;
+                    v[r][4] = b.x; v[r][5] = b.y; v[r][6] = b.z; v[r][7] = b.w;
+                    dA[r] = __uint_as_float(s.x);
+                    dB[r] = __uint_as_float(s.y);
+                }
+            }
+
+            float xr[64];
+            const float4* xq = reinterpret_cast<const float4*>(xs + xpad(pc * 64));
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const float4 t = xq[q];
+                xr[4 * q] = t.x; xr[4 * q + 1] = t.y; xr[4 * q + 2] = t.z; xr[4 * q + 3] = t.w;
+            }
+            const float bA = bias[2 * pc], bB = bias[2 * pc + 1];
+
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float tA = 0.f, tB = 0.f;
+                if (kGguf) {
+                    dA[r] = half_lo(v[r][0]);
+                    dB[r] = half_hi(v[r][4]);
+                    tA = q4_bytes<2, 4, 0>(v[r][0], xr, xr + 16, tA);
+                    tA = q4_bytes<0, 4, 2>(v[r][1], xr, xr + 16, tA);
+                    tA = q4_bytes<0, 4, 6>(v[r][2], xr, xr + 16, tA);
+                    tA = q4_bytes<0, 4, 10>(v[r][3], xr, xr + 16, tA);
+                    tA = q4_bytes<0, 2, 14>(v[r][4], xr, xr + 16, tA);
+                    tB = q4_bytes<0, 4, 0>(v[r][5], xr + 32, xr + 48, tB);
+                    tB = q4_bytes<0, 4, 4>(v[r][6], xr + 32, xr + 48, tB);
+                    tB = q4_bytes<0, 4, 8>(v[r][7], xr + 32, xr + 48, tB);
+                    tB = q4_bytes<0, 4, 12>(v[r][8], xr + 32, xr + 48, tB);
+                } else {
+                    tA = q4_bytes<0, 4, 0>(v[r][0], xr, xr + 16, tA);
+                    tA = q4_bytes<0, 4, 4>(v[r][1], xr, xr + 16, tA);
+                    tA = q4_bytes<0, 4, 8>(v[r][2], xr, xr + 16, tA);
+                    tA = q4_bytes<0, 4, 12>(v[r][3], xr, xr + 16, tA);
+                    tB = q4_bytes<0, 4, 0>(v[r][4], xr + 32, xr + 48, tB);
+                    tB = q4_bytes<0, 4, 4>(v[r][5], xr + 32, xr + 48, tB);
+                    tB = q4_bytes<0, 4, 8>(v[r][6], xr + 32, xr + 48, tB);
+                    tB = q4_bytes<0, 4, 12>(v[r][7], xr + 32, xr + 48, tB);
+                }
+                float a = fmaf(dA[r], tA - bA, acc[r]);
+                a = fmaf(dB[r], tB - bB, a);
+                acc[r] = active ? a : acc[r];
+            }
+        }
+
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float s = wave_sum(acc[r]);
+            if (lane == r && row0 + r < M) y[row0 + r] = s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 pair kernel.  kGguf: 34-byte blocks; otherwise split qs + fp32 scales.
+// ---------------------------------------------------------------------------
+template <int R, bool kGguf>
+__global__ __launch_bounds__(kThreads) void q8_matvec_pairs(const uint8_t* __restrict__ w,
+                                                            const float* __restrict__ wscale,
+                                                            const float* __restrict__ x,
+                                                            float* __restrict__ y, int M, int K) {
+    extern __shared__ float smem[];
+    float* xs = smem;
+    float* bias = smem + K + (K >> 4);
+    stage_x<false>(x, xs, bias, K);
+
+    const int nb = K >> 5;
+    const int np = nb >> 1;
+    const uint32_t row_bytes = kGguf ? (uint32_t)nb * 34u : (uint32_t)nb * 32u;
+    const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
+    const auto sr = make_rsrc(wscale, kGguf ? 0u : (uint32_t)nb * 4u * (uint32_t)M);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nwaves = gridDim.x * kWavesPerBlock;
+
+    for (int g = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6); g * R < M; g += nwaves) {
+        const int row0 = g * R;
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+
+        for (int c0 = 0; c0 < np; c0 += kWave) {
+            const int p = c0 + lane;
+            const bool active = p < np;
+            const int pc = active ? p : np - 1;
+
+            uint32_t v[R][17];
+            float dA[R], dB[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = min(row0 + r, M - 1);
+                if (kGguf) {
+                    const uint32_t off = (uint32_t)row * row_bytes + (uint32_t)pc * 68u;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint4 a = buf_load_b128(wr, off + 16u * q);
+                        v[r][4 * q] = a.x; v[r][4 * q + 1] = a.y; v[r][4 * q + 2] = a.z; v[r][4 * q + 3] = a.w;
+                    }
+                    v[r][16] = buf_load_b32(wr, off + 64u);
+                } else {
+                    const uint32_t blk = (uint32_t)row * (uint32_t)nb + 2u * (uint32_t)pc;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint4 a = buf_load_b128(wr, blk * 32u + 16u * q);
+                        v[r][4 * q] = a.x; v[r][4 * q + 1] = a.y; v[r][4 * q + 2] = a.z; v[r][4 * q + 3] = a.w;
+                    }
+                    const uint2 s = buf_load_b64(sr, blk * 4u);
+                    dA[r] = __uint_as_float(s.x);
+                    dB[r] = __uint_as_float(s.y);
+                }
+            }
+
+            float xr[64];
+            const float4* xq = reinterpret_cast<const float4*>(xs + xpad(pc * 64));
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const float4 t = xq[q];
+                xr[4 * q] = t.x; xr[4 * q + 1] = t.y; xr[4 * q + 2] = t.z; xr[4 * q + 3] = t.w;
+            }
+            const float bA = bias[2 * pc], bB = bias[2 * pc + 1];
+
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float tA = 0.f, tB = 0.f;
+                if (kGguf) {
+                    // v0 = [dA | q0 q1], v1..v7 = q2..q29, v8 = [q30 q31 | dB], v9..v16 = block B.
+                    dA[r] = half_lo(v[r][0]);
+                    dB[r] = half_hi(v[r][8]);
+                    tA = q8_bytes<2, 4, 0>(v[r][0], xr, tA);
+#pragma unroll
+                    for (int q = 1; q < 8; ++q) tA = q8_bytes<0, 4, 0>(v[r][q], xr + 2 + 4 * (q - 1), tA);
+                    tA = q8_bytes<0, 2, 30>(v[r][8], xr, tA);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) tB = q8_bytes<0, 4, 0>(v[r][9 + q], xr + 32 + 4 * q, tB);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) tA = q8_bytes<0, 4, 0>(v[r][q], xr + 4 * q, tA);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) tB = q8_bytes<0, 4, 0>(v[r][8 + q], xr + 32 + 4 * q, tB);
+                }
+                float a = fmaf(dA[r], tA - bA, acc[r]);
+                a = fmaf(dB[r], tB - bB, a);
+                acc[r] = active ? a : acc[r];
+            }
+        }
+
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float s = wave_sum(acc[r]);
+            if (lane == r && row0 + r < M) y[row0 + r] = s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernel: one wave per row, one block per lane, byte loads.  Covers
+// what the pair kernels do not (odd K/32, rows not dword aligned, x too large
+// for LDS).  Correct for every K % 32 == 0, not tuned.
+// ---------------------------------------------------------------------------
+template <bool kQ8, bool kGguf>
+__global__ __launch_bounds__(kThreads) void matvec_generic(const uint8_t* __restrict__ w,
+                                                           const float* __restrict__ wscale,
+                                                           const float* __restrict__ x,
+                                                           float* __restrict__ y, int M, int K) {
+    const int nb = K >> 5;
+    const int qbytes = kQ8 ? 32 : 16;
+    const int64_t blk_bytes = kGguf ? qbytes + 2 : qbytes;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    if (row >= M) return;
+    float acc = 0.f;
+    for (int b = lane; b < nb; b += kWave) {
+        const int64_t blk = (int64_t)row * nb + b;
+        const uint8_t* p = w + blk * blk_bytes;
+        float d;
+        if (kGguf) {
+            d = __half2float(__ushort_as_half((unsigned short)(p[0] | (p[1] << 8))));
+            p += 2;
+        } else {
+            d = wscale[blk];
+        }
+        const float* xb = x + (int64_t)b * 32;
+        float t = 0.f;
+        if (kQ8) {
+            for (int j = 0; j < 32; ++j) t = fmaf((float)(int8_t)p[j], xb[j], t);
+        } else {
+            for (int j = 0; j < 16; ++j) {
+                t = fmaf((float)(int)(p[j] & 15) - 8.0f, xb[j], t);
+                t = fmaf((float)(int)(p[j] >> 4) - 8.0f, xb[16 + j], t);
+            }
+        }
+        acc = fmaf(d, t, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Exact dequantization: one thread per block.
+// ---------------------------------------------------------------------------
+template <bool kQ8>
+__global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
+                                                           int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint8_t* p = w + i * (kQ8 ? 34 : 18);
+    const float d = __half2float(__ushort_as_half((unsigned short)(p[0] | (p[1] << 8))));
+    float* o = out + i * 32;
+    if (kQ8) {
+        for (int j = 0; j < 32; ++j) o[j] = (float)(int8_t)p[2 + j] * d;
+    } else {
+        for (int j = 0; j < 16; ++j) {
+            o[j] = ((float)(int)(p[2 + j] & 15) - 8.0f) * d;
+            o[16 + j] = ((float)(int)(p[2 + j] >> 4) - 8.0f) * d;
+        }
+    }
+}
+
+size_t pair_lds_bytes(int64_t K) { return (size_t)(K + K / 16 + K / 32) * sizeof(float); }
+
+int pick_rows_per_wave(int64_t M, int r_max) {
+    // Aim for at least ~8 waves per CU across 256 CUs before growing R.
+    int r = r_max;
+    while (r > 1 && (M + r - 1) / r < 2048) r >>= 1;
+    return r;
+}
+
+template <int R, bool kGguf>
+void launch_q4(const uint8_t* w, const float* s, const float* x, float* y, int M, int K, size_t lds,
+               hipStream_t st) {
+    const int64_t groups = (M + R - 1) / R;
+    const int blocks = (int)((groups + kWavesPerBlock - 1) / kWavesPerBlock);
+    hipLaunchKernelGGL((q4_matvec_pairs<R, kGguf>), dim3(blocks), dim3(kThreads), lds, st, w, s, x, y, M, K);
+}
+
+template <int R, bool kGguf>
+void launch_q8(const uint8_t* w, const float* s, const float* x, float* y, int M, int K, size_t lds,
+               hipStream_t st) {
+    const int64_t groups = (M + R - 1) / R;
+    const int blocks = (int)((groups + kWavesPerBlock - 1) / kWavesPerBlock);
+    hipLaunchKernelGGL((q8_matvec_pairs<R, kGguf>), dim3(blocks), dim3(kThreads), lds, st, w, s, x, y, M, K);
+}
+
+bool lds_opt_in_done = false;
+
+}  // namespace
+
+int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, const float* x, float* y,
+                  int64_t M, int64_t K, hipStream_t stream) {
+    if (M <= 0 || K <= 0 || (K % 32) != 0)
+        return fail(kInvalidArgument, "matvec: need M > 0, K > 0 and K %% 32 == 0 (got M=%lld K=%lld)",
+                    (long long)M, (long long)K);
+    if (M > INT32_MAX || K > INT32_MAX) return fail(kInvalidArgument, "matvec: M and K must fit in int32");
+    const int64_t nb = K / 32;
+    const int64_t blk_bytes = qt == QuantType::Q4_0 ? (gguf ? 18 : 16) : (gguf ? 34 : 32);
+    const int64_t total = M * nb * blk_bytes;
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    const size_t lds = pair_lds_bytes(K);
+    const bool aligned = ((uintptr_t)w % 4 == 0) && (!gguf || nb % 2 == 0) && ((uintptr_t)scales % 8 == 0) &&
+                         ((uintptr_t)x % 4 == 0);
+    const bool pairs = nb % 2 == 0 && aligned && lds <= 160 * 1024 && total < (int64_t)UINT32_MAX;
+    const int m = (int)M, k = (int)K;
+
+    if (!lds_opt_in_done) {
+        // Dynamic LDS beyond 64 KB needs an explicit opt-in per kernel.
+        const int max_lds = 160 * 1024;
+        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<1, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<2, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<4, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<8, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<1, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<2, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<4, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<8, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<1, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<2, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<4, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<1, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<2, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<4, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
+        lds_opt_in_done = true;
+    }
+
+    if (pairs && qt == QuantType::Q4_0) {
+        const int r = pick_rows_per_wave(M, 8);
+        if (gguf) {
+            switch (r) {
+                case 8: launch_q4<8, true>(wb, scales, x, y, m, k, lds, stream); break;
+                case 4: launch_q4<4, true>(wb, scales, x, y, m, k, lds, stream); break;
+                case 2: launch_q4<2, true>(wb, scales, x, y, m, k, lds, stream); break;
+                default: launch_q4<1, true>(wb, scales, x, y, m, k, lds, stream); break;
+            }
+        } else {
+            switch (r) {
+                case 8: launch_q4<8, false>(wb, scales, x, y, m, k, lds, stream); break;
+                case 4: launch_q4<4, false>(wb, scales, x, y, m, k, lds, stream); break;
+                case 2: launch_q4<2, false>(wb, scales, x, y, m, k, lds, stream); break;
+                default: launch_q4<1, false>(wb, scales, x, y, m, k, lds, stream); break;
+            }
+        }
+    } else if (pairs) {
+        const int r = pick_rows_per_wave(M, 4);
+        if (gguf) {
+            switch (r) {
+                case 4: launch_q8<4, true>(wb, scales, x, y, m, k, lds, stream); break;
+                case 2: launch_q8<2, true>(wb, scales, x, y, m, k, lds, stream); break;
+                default: launch_q8<1, true>(wb, scales, x, y, m, k, lds, stream); break;
+            }
+        } else {
+            switch (r) {
+                case 4: launch_q8<4, false>(wb, scales, x, y, m, k, lds, stream); break;
+                case 2: launch_q8<2, false>(wb, scales, x, y, m, k, lds, stream); break;
+                default: launch_q8<1, false>(wb, scales, x, y, m, k, lds, stream); break;
+            }
+        }
+    } else {
+        const int blocks = (int)((M + kWavesPerBlock - 1) / kWavesPerBlock);
+        if (qt == QuantType::Q4_0) {
+            if (gguf)
+                hipLaunchKernelGGL((matvec_generic<false, true>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k);
+            else
+                hipLaunchKernelGGL((matvec_generic<false, false>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k);
+        } else {
+            if (gguf)
+                hipLaunchKernelGGL((matvec_generic<true, true>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k);
+            else
+                hipLaunchKernelGGL((matvec_generic<true, false>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k);
+        }
+    }
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int dequant_launch(QuantType qt, const void* w, float* out, int64_t rows, int64_t K, hipStream_t stream) {
+    if (rows <= 0 || K <= 0 || (K % 32) != 0)
+        return fail(kInvalidArgument, "dequantize: need rows > 0, K > 0 and K %% 32 == 0");
+    const int64_t nblocks = rows * (K / 32);
+    const int64_t grid = (nblocks + kThreads - 1) / kThreads;
+    if (grid > INT32_MAX) return fail(kInvalidArgument, "dequantize: tensor too large");
+    if (qt == QuantType::Q4_0)
+        hipLaunchKernelGGL((dequant_kernel<false>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                           static_cast<const uint8_t*>(w), out, nblocks);
+    else
+        hipLaunchKernelGGL((dequant_kernel<true>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                           static_cast<const uint8_t*>(w), out, nblocks);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+}  // namespace asmhip

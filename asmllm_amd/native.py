@@ -1,0 +1,115 @@
+"""ctypes binding of libasmllm.so.
+
+Mirrors the reference's loader (tests/correctness/test_runner.py:52-68) and the
+argtypes its callers set (test_runner.py:94-101, 199-207, 384-390, 408-414,
+430, 448-456; src/runtime/generate.py:221-250).  The reference loads
+``build/libasmllm.so``; this package loads ``asmllm_amd/lib/libasmllm.so``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p, c_char_p, POINTER
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "lib" / "libasmllm.so"
+HEADER_PATH = PKG.parent / "include" / "asmllm_hip.h"
+
+_P = c_void_p
+# name -> (restype, argtypes)
+SIGNATURES: dict[str, tuple] = {
+    # reference-named entry points
+    "asm_matmul_q4": (None, [_P, _P, _P, _P, c_int64, c_int64]),
+    "asm_matmul_q4_avx512": (None, [_P, _P, _P, _P, c_int64, c_int64]),
+    "asm_matmul_q8": (None, [_P, _P, _P, _P, c_int64, c_int64]),
+    "asm_matmul_q4_mt": (None, [_P, _P, _P, _P, c_int64, c_int64, c_int]),
+    "asm_matmul_q8_mt": (None, [_P, _P, _P, _P, c_int64, c_int64, c_int]),
+    "asm_threadpool_dispatch_q8": (None, [_P, _P, _P, _P, c_int64, c_int64]),
+    "asm_threadpool_init": (None, [c_int]),
+    "asm_threadpool_shutdown": (None, []),
+    "asm_threadpool_get_num_threads": (c_int, []),
+    # device entry points
+    "asmhip_matmul_q4_0": (c_int, [_P, _P, _P, c_int64, c_int64, _P]),
+    "asmhip_matmul_q8_0": (c_int, [_P, _P, _P, c_int64, c_int64, _P]),
+    "asmhip_matmul_q4_split": (c_int, [_P, _P, _P, _P, c_int64, c_int64, _P]),
+    "asmhip_matmul_q8_split": (c_int, [_P, _P, _P, _P, c_int64, c_int64, _P]),
+    "asmhip_dequantize_q4_0": (c_int, [_P, _P, c_int64, c_int64, _P]),
+    "asmhip_dequantize_q8_0": (c_int, [_P, _P, c_int64, c_int64, _P]),
+    # plumbing
+    "asmhip_device_count": (c_int, []),
+    "asmhip_device_info": (c_int, [c_char_p, c_size_t, POINTER(c_int), POINTER(c_int), POINTER(c_size_t)]),
+    "asmhip_malloc": (c_void_p, [c_size_t]),
+    "asmhip_free": (c_int, [_P]),
+    "asmhip_memcpy": (c_int, [_P, _P, c_size_t, c_int]),
+    "asmhip_synchronize": (c_int, []),
+    "asmhip_stream_create": (c_void_p, []),
+    "asmhip_stream_destroy": (c_int, [_P]),
+    "asmhip_stream_synchronize": (c_int, [_P]),
+    "asmhip_event_create": (c_void_p, []),
+    "asmhip_event_destroy": (c_int, [_P]),
+    "asmhip_event_record": (c_int, [_P, _P]),
+    "asmhip_event_synchronize": (c_int, [_P]),
+    "asmhip_event_elapsed_ms": (c_int, [_P, _P, POINTER(c_float)]),
+    "asmhip_stream_begin_capture": (c_int, [_P]),
+    "asmhip_stream_end_capture": (c_int, [_P, POINTER(c_void_p)]),
+    "asmhip_graph_launch": (c_int, [_P, _P]),
+    "asmhip_graph_destroy": (c_int, [_P]),
+    "asmhip_last_error": (c_char_p, []),
+}
+
+
+class NativeError(RuntimeError):
+    """A libasmllm entry point returned a non-zero status."""
+
+
+def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return lib
+
+
+def try_load_native_library() -> ctypes.CDLL | None:
+    """Returns the loaded library, or None when it has not been built
+    (the reference's "NOT IMPLEMENTED" convention, test_runner.py:52-68)."""
+    if not LIB_PATH.exists():
+        return None
+    try:
+        return declare(ctypes.CDLL(str(LIB_PATH)))
+    except OSError:
+        return None
+
+
+_LIB: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it is missing (no silent fallback)."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -m asmllm_amd.build`")
+        _LIB = declare(ctypes.CDLL(str(LIB_PATH)))
+    return _LIB
+
+
+def last_error() -> str:
+    msg = lib().asmhip_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(status: int, what: str = "") -> None:
+    if status != 0:
+        raise NativeError(f"{what or 'libasmllm call'} failed ({status}): {last_error()}")
+
+
+def header_symbols(path: Path = HEADER_PATH) -> list[str]:
+    """Every function the public header declares."""
+    import re
+
+    text = path.read_text()
+    return re.findall(r"ASMHIP_API\s+[\w\s\*]+?\b(\w+)\s*\(", text)

@@ -1,0 +1,132 @@
+/*
+ * asmllm_hip.h -- C ABI of libasmllm.so, the MI355X (gfx950) build of asmllm's
+ * quantized matvec path.
+ *
+ * Two groups of entry points:
+ *
+ *  1. Reference-named, synchronous entry points.  Same names, argument order
+ *     and meaning as the symbols asmllm's ctypes callers bind (export list
+ *     build_kernel.py:85-104, argtypes tests/correctness/test_runner.py:84-475,
+ *     src/runtime/generate.py:221-250).  Each accepts host pointers (numpy
+ *     buffers: staged through device memory) or device pointers, computes on
+ *     the GPU, and returns with the result in place, as the reference's
+ *     kernels do.  They return void like the reference; an error is printed
+ *     to stderr, y is left untouched and asmhip_last_error() describes it.
+ *
+ *  2. asmhip_* device entry points: device pointers only, stream-ordered
+ *     (stream NULL = HIP's default stream), no synchronization, return 0 or a
+ *     negative status.  Weights stay resident in HBM in their GGUF block
+ *     layout; these are the hot path.
+ *
+ * Block layouts (GGUF):  Q4_0 = fp16 d + 16 bytes, byte j holding weight j
+ * (low nibble) and weight j+16 (high nibble), value (nibble - 8) * d;
+ * Q8_0 = fp16 d + 32 int8, value q * d.  Rows are [M][K/32] blocks.
+ * Split layout (the reference kernels' ABI): qs [M][K/32][16 or 32] bytes
+ * plus fp32 scales [M][K/32].  K must be a multiple of 32.
+ */
+#ifndef ASMLLM_HIP_H
+#define ASMLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ASMHIP_API __attribute__((visibility("default")))
+
+/* Status codes of the asmhip_* entry points. */
+#define ASMHIP_OK 0
+#define ASMHIP_ERR_INVALID_ARGUMENT (-1)
+#define ASMHIP_ERR_HIP (-2)
+#define ASMHIP_ERR_UNSUPPORTED (-3)
+#define ASMHIP_ERR_NO_DEVICE (-4)
+
+/* ---- 1. reference-named entry points ------------------------------------ */
+
+/* src/kernels/x86_64/matmul_q4_avx2.asm:11-19, 57: y = W x, split layout. */
+ASMHIP_API void asm_matmul_q4(const uint8_t* qweights, const float* scales, const float* x, float* y,
+                              int64_t M, int64_t K);
+/* src/kernels/x86_64/matmul_q4_avx512.asm:57 (same contract as asm_matmul_q4). */
+ASMHIP_API void asm_matmul_q4_avx512(const uint8_t* qweights, const float* scales, const float* x,
+                                     float* y, int64_t M, int64_t K);
+/* src/kernels/x86_64/matmul_q8_avx2.asm:11-19, 51. */
+ASMHIP_API void asm_matmul_q8(const int8_t* qweights, const float* scales, const float* x, float* y,
+                              int64_t M, int64_t K);
+/* src/runtime/threadpool.h:49-57 / threadpool.c:390-486.  On the GPU one
+ * launch covers all rows; num_threads only updates the recorded pool size
+ * (threadpool.c:404-406), the result is bitwise the same for every value. */
+ASMHIP_API void asm_matmul_q4_mt(const uint8_t* qweights, const float* scales, const float* x, float* y,
+                                 int64_t M, int64_t K, int num_threads);
+/* src/runtime/threadpool.h:59-67 / threadpool.c:750-767. */
+ASMHIP_API void asm_matmul_q8_mt(const int8_t* qweights, const float* scales, const float* x, float* y,
+                                 int64_t M, int64_t K, int num_threads);
+/* src/runtime/threadpool.h:80-87 / threadpool.c:588-665. */
+ASMHIP_API void asm_threadpool_dispatch_q8(const int8_t* qweights, const float* scales, const float* x,
+                                           float* y, int64_t M, int64_t K);
+/* src/runtime/threadpool.h:37 / threadpool.c:340-369: binds the calling
+ * thread's current HIP device, creates the library stream and records the
+ * pool size (clamped to [1, 64], threadpool.c:345-346). */
+ASMHIP_API void asm_threadpool_init(int num_threads);
+/* src/runtime/threadpool.h:42 / threadpool.c:371-382: drains and releases
+ * the library stream and staging memory; pool size becomes 0. */
+ASMHIP_API void asm_threadpool_shutdown(void);
+/* src/runtime/threadpool.h:102 / threadpool.c:386-388. */
+ASMHIP_API int asm_threadpool_get_num_threads(void);
+
+/* ---- 2. device entry points (hot path) ----------------------------------- */
+
+/* Q4_0 matvec over GGUF blocks resident in HBM: y[M] = W[M][K] x[K].  Block
+ * arithmetic of matmul_q4_avx2.asm:110-178 with the GGUF scale widened
+ * fp16 -> fp32 (src/runtime/generate.py:91-106). */
+ASMHIP_API int asmhip_matmul_q4_0(const void* blocks, const float* x, float* y, int64_t M, int64_t K,
+                                  void* stream);
+/* Q8_0 matvec over GGUF blocks (matmul_q8_avx2.asm:103-155, generate.py:109-119). */
+ASMHIP_API int asmhip_matmul_q8_0(const void* blocks, const float* x, float* y, int64_t M, int64_t K,
+                                  void* stream);
+/* Split-layout matvecs on device pointers (the asm_matmul_q4 / asm_matmul_q8
+ * contract without staging or synchronization). */
+ASMHIP_API int asmhip_matmul_q4_split(const uint8_t* qweights, const float* scales, const float* x,
+                                      float* y, int64_t M, int64_t K, void* stream);
+ASMHIP_API int asmhip_matmul_q8_split(const int8_t* qweights, const float* scales, const float* x,
+                                      float* y, int64_t M, int64_t K, void* stream);
+/* Exact fp32 dequantization of GGUF blocks into w[rows][K]
+ * (tests/reference/ops.py:16-30, 44-53). */
+ASMHIP_API int asmhip_dequantize_q4_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream);
+ASMHIP_API int asmhip_dequantize_q8_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream);
+
+/* ---- device memory, streams, events (so a ctypes host needs no other GPU
+ *      binding; the reference's buffers are numpy arrays) ----------------- */
+
+ASMHIP_API int asmhip_device_count(void);
+/* Name, compute units, peak engine clock (kHz) and memory of the current device. */
+ASMHIP_API int asmhip_device_info(char* name, size_t name_len, int* compute_units, int* clock_khz,
+                                  size_t* total_mem);
+ASMHIP_API void* asmhip_malloc(size_t bytes);
+ASMHIP_API int asmhip_free(void* ptr);
+/* kind: 1 host->device, 2 device->host, 3 device->device.  Synchronous. */
+ASMHIP_API int asmhip_memcpy(void* dst, const void* src, size_t bytes, int kind);
+ASMHIP_API int asmhip_synchronize(void);
+ASMHIP_API void* asmhip_stream_create(void);
+ASMHIP_API int asmhip_stream_destroy(void* stream);
+ASMHIP_API int asmhip_stream_synchronize(void* stream);
+ASMHIP_API void* asmhip_event_create(void);
+ASMHIP_API int asmhip_event_destroy(void* event);
+ASMHIP_API int asmhip_event_record(void* event, void* stream);
+ASMHIP_API int asmhip_event_synchronize(void* event);
+ASMHIP_API int asmhip_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Stream capture into a HIP graph: begin on a stream, enqueue work, end to
+ * get an instantiated graph that asmhip_graph_launch replays on any stream. */
+ASMHIP_API int asmhip_stream_begin_capture(void* stream);
+ASMHIP_API int asmhip_stream_end_capture(void* stream, void** graph_exec);
+ASMHIP_API int asmhip_graph_launch(void* graph_exec, void* stream);
+ASMHIP_API int asmhip_graph_destroy(void* graph_exec);
+/* Message for the calling thread's last failed call ("" if none). */
+ASMHIP_API const char* asmhip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASMLLM_HIP_H */

@@ -1,0 +1,63 @@
+"""Host-side logic (no GPU): GGUF layouts and quantizers, the C-ABI library's
+exports, and the Python binding's coverage of the public header."""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from asmllm_amd import gguf, native
+from conftest import GOLDEN_DIR
+
+
+def test_numpy_quantizers_match_oracle_bitwise(oracle):
+    rng = np.random.default_rng(21)
+    w = (rng.standard_normal((257, 512)) * 0.02).astype(np.float32)
+    w[3, :32] = 0.0                  # all-zero block
+    w[4, 40] = -w[4, 32:64].__abs__().max() * 2  # negative peak
+    np.testing.assert_array_equal(gguf.quantize_q4_0(w), oracle.quantize_q4_0(w))
+    np.testing.assert_array_equal(gguf.quantize_q8_0(w), oracle.quantize_q8_0(w))
+
+
+def test_numpy_quantizers_known_answers():
+    with np.load(GOLDEN_DIR / "quant_known_answers.npz") as f:
+        np.testing.assert_array_equal(gguf.quantize_q4_0(f["q4_w"]), f["q4_blocks"])
+        np.testing.assert_array_equal(gguf.quantize_q8_0(f["q8_w"]), f["q8_blocks"])
+
+
+def test_split_and_dequant_match_oracle(oracle):
+    rng = np.random.default_rng(22)
+    w = (rng.standard_normal((33, 256)) * 0.02).astype(np.float32)
+    b4, b8 = gguf.quantize_q4_0(w), gguf.quantize_q8_0(w)
+    for mine, theirs in zip(gguf.split_q4_0(b4), oracle.split_q4_0(b4)):
+        np.testing.assert_array_equal(mine, theirs)
+    for mine, theirs in zip(gguf.split_q8_0(b8), oracle.split_q8_0(b8)):
+        np.testing.assert_array_equal(mine, theirs)
+    np.testing.assert_array_equal(gguf.dequantize_q4_0(b4), oracle.dequantize_q4_0(b4))
+    np.testing.assert_array_equal(gguf.dequantize_q8_0(b8), oracle.dequantize_q8_0(b8))
+
+
+def test_quantize_rejects_ragged_k():
+    with pytest.raises(ValueError):
+        gguf.quantize_q4_0(np.zeros((2, 33), np.float32))
+
+
+def test_library_exports_every_header_symbol():
+    lib = native.try_load_native_library()
+    assert lib is not None, f"{native.LIB_PATH} not built (python -m asmllm_amd.build)"
+    declared = native.header_symbols()
+    assert len(declared) >= 30
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, f"declared in include/asmllm_hip.h but not exported: {missing}"
+
+
+def test_binding_covers_header_exactly():
+    assert sorted(native.SIGNATURES) == sorted(native.header_symbols())
+
+
+def test_reference_argtypes_mirrored():
+    # test_runner.py:94-101 (matvec) and :199-207 (_mt) argtypes
+    P, I64 = ctypes.c_void_p, ctypes.c_int64
+    assert native.SIGNATURES["asm_matmul_q4"] == (None, [P, P, P, P, I64, I64])
+    assert native.SIGNATURES["asm_matmul_q8"] == (None, [P, P, P, P, I64, I64])
+    assert native.SIGNATURES["asm_matmul_q4_mt"] == (None, [P, P, P, P, I64, I64, ctypes.c_int])

@@ -1,0 +1,294 @@
+"""Pins the CPU oracle (test infrastructure) before it is trusted as the checker.
+
+Each restated function is checked against at least one of: the reference's
+golden inputs with its own tolerances (tests/correctness/test_runner.py:33-36),
+a float64 closed form, an exact special case, or a second independently
+written per-lane model of the same SIMD arithmetic.
+"""
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN_DIR, assert_matvec_close
+from oracle import golden as golden_mod
+from oracle import ops_ref
+
+
+def _rand_q4(rng, M, K):
+    q = rng.integers(0, 256, size=(M, K // 32, 16), dtype=np.uint8)
+    s = rng.uniform(0.05, 0.25, size=(M, K // 32)).astype(np.float32)
+    return q, s
+
+
+def _rand_q8(rng, M, K):
+    q = rng.integers(-128, 128, size=(M, K // 32, 32), dtype=np.int8)
+    s = rng.uniform(0.05, 0.25, size=(M, K // 32)).astype(np.float32)
+    return q, s
+
+
+# ---- golden vectors (reference_gen.py recipe, test_runner.py tolerances) ----------
+
+def test_golden_fixture_matches_recipe(golden):
+    fresh = golden_mod.generate_reference_data(42)
+    assert sorted(fresh) == sorted(golden)
+    for k in golden:
+        np.testing.assert_array_equal(fresh[k], golden[k], err_msg=k)
+
+
+@pytest.mark.parametrize("kernel", ["avx2", "lanes", "avx512", "avx512_lanes"])
+def test_q4_golden(oracle, golden, kernel):
+    y = oracle.matmul_q4(golden["q4_matmul_qweights"], golden["q4_matmul_scales"], golden["q4_matmul_x"], kernel)
+    err = np.abs(y - golden["q4_matmul_expected"]).max()
+    assert err <= golden_mod.TOLERANCE_Q4
+    assert err <= 1e-4  # fp32 reassociation only
+
+
+@pytest.mark.parametrize("kernel", ["avx2", "lanes"])
+def test_q8_golden(oracle, golden, kernel):
+    y = oracle.matmul_q8(golden["q8_matmul_qweights"], golden["q8_matmul_scales"], golden["q8_matmul_x"], kernel)
+    err = np.abs(y - golden["q8_matmul_expected"]).max()
+    assert err <= golden_mod.TOLERANCE_Q8
+
+
+def test_golden_q4_expected_against_float64(golden):
+    y64 = ops_ref.q4_matvec_f64(golden["q4_matmul_qweights"], golden["q4_matmul_scales"], golden["q4_matmul_x"])
+    np.testing.assert_allclose(golden["q4_matmul_expected"], y64, rtol=0, atol=1e-4)
+
+
+def test_decode_ops_golden(oracle, golden):
+    tol = golden_mod.TOLERANCE_FP32
+    y = oracle.rmsnorm(golden["rmsnorm_x"], golden["rmsnorm_weight"], float(golden["rmsnorm_eps"]))
+    assert np.abs(y - golden["rmsnorm_expected"]).max() <= tol
+    q, k = oracle.rope(golden["rope_q"], golden["rope_k"], 32, int(golden["rope_pos"]), 10000.0)
+    assert max(np.abs(q - golden["rope_q_expected"]).max(), np.abs(k - golden["rope_k_expected"]).max()) <= tol
+    y = oracle.softmax(golden["softmax_x"])
+    assert np.abs(y - golden["softmax_expected"]).max() <= tol
+    a = oracle.attention(golden["attention_q"], golden["attention_k"], golden["attention_v"], 1.0 / np.sqrt(16))
+    assert np.abs(a - golden["attention_expected"]).max() <= tol
+
+
+# ---- SIMD restatements against their per-lane models (bitwise) ----------------------
+
+@pytest.mark.parametrize("M,K", [(1, 32), (7, 64), (33, 256), (64, 4096)])
+def test_q4_avx2_equals_lane_model(oracle, M, K):
+    rng = np.random.default_rng(M * 1000 + K)
+    q, s = _rand_q4(rng, M, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    np.testing.assert_array_equal(oracle.matmul_q4(q, s, x, "avx2"), oracle.matmul_q4(q, s, x, "lanes"))
+    np.testing.assert_array_equal(oracle.matmul_q4(q, s, x, "avx512"), oracle.matmul_q4(q, s, x, "avx512_lanes"))
+
+
+@pytest.mark.parametrize("M,K", [(1, 32), (9, 128), (64, 4096)])
+def test_q8_avx2_equals_lane_model(oracle, M, K):
+    rng = np.random.default_rng(M + K)
+    q, s = _rand_q8(rng, M, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    np.testing.assert_array_equal(oracle.matmul_q8(q, s, x, "avx2"), oracle.matmul_q8(q, s, x, "lanes"))
+
+
+def test_avx2_and_avx512_orders_differ_but_agree(oracle):
+    rng = np.random.default_rng(5)
+    q, s = _rand_q4(rng, 256, 4096)
+    x = rng.standard_normal(4096).astype(np.float32)
+    a, b = oracle.matmul_q4(q, s, x, "avx2"), oracle.matmul_q4(q, s, x, "avx512")
+    assert_matvec_close(a, b, ops_ref.dequantize_q4_0(q, s), x, rel=1e-6)
+
+
+# ---- float64 closed forms -----------------------------------------------------------
+
+@pytest.mark.parametrize("M,K", [(16, 4096), (8, 11008)])
+def test_q4_against_float64(oracle, M, K):
+    rng = np.random.default_rng(K)
+    q, s = _rand_q4(rng, M, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    y64 = ops_ref.q4_matvec_f64(q, s, x)
+    for kern in ("avx2", "avx512"):
+        assert_matvec_close(oracle.matmul_q4(q, s, x, kern), y64, ops_ref.dequantize_q4_0(q, s), x, rel=1e-6)
+
+
+def test_q8_against_float64(oracle):
+    rng = np.random.default_rng(8)
+    q, s = _rand_q8(rng, 16, 4096)
+    x = rng.standard_normal(4096).astype(np.float32)
+    assert_matvec_close(oracle.matmul_q8(q, s, x), ops_ref.q8_matvec_f64(q, s, x), ops_ref.dequantize_q8_0(q, s), x,
+                        rel=1e-6)
+
+
+def test_closed_form_catches_swapped_nibbles(oracle):
+    """A plausible mistake -- low/high nibble halves swapped -- must fail the bar."""
+    rng = np.random.default_rng(11)
+    q, s = _rand_q4(rng, 8, 256)
+    x = rng.standard_normal(256).astype(np.float32)
+    swapped = ((q & 0x0F) << 4) | (q >> 4)
+    y_bad = oracle.matmul_q4(swapped, s, x)
+    l1 = np.abs(ops_ref.dequantize_q4_0(q, s).astype(np.float64)) @ np.abs(x.astype(np.float64))
+    assert np.any(np.abs(y_bad - ops_ref.q4_matvec_f64(q, s, x)) > 1e-4 * l1)
+
+
+# ---- exact special cases ---------------------------------------------------------------
+
+def test_q4_all_eight_is_zero(oracle):
+    q = np.full((5, 4, 16), 0x88, np.uint8)
+    s = np.ones((5, 4), np.float32)
+    x = np.random.default_rng(1).standard_normal(128).astype(np.float32)
+    assert np.all(oracle.matmul_q4(q, s, x) == 0.0)
+
+
+def test_q4_zero_scale_is_zero(oracle):
+    rng = np.random.default_rng(2)
+    q, _ = _rand_q4(rng, 5, 128)
+    x = rng.standard_normal(128).astype(np.float32)
+    assert np.all(oracle.matmul_q4(q, np.zeros((5, 4), np.float32), x) == 0.0)
+
+
+@pytest.mark.parametrize("col", [0, 5, 16, 31, 63])
+def test_q4_one_hot_picks_column(oracle, col):
+    rng = np.random.default_rng(col)
+    q, s = _rand_q4(rng, 6, 64)
+    x = np.zeros(64, np.float32)
+    x[col] = 1.0
+    w = ops_ref.dequantize_q4_0(q, s)
+    np.testing.assert_array_equal(oracle.matmul_q4(q, s, x), w[:, col])
+
+
+@pytest.mark.parametrize("col", [0, 17, 40])
+def test_q8_one_hot_picks_column(oracle, col):
+    rng = np.random.default_rng(col)
+    q, s = _rand_q8(rng, 6, 64)
+    x = np.zeros(64, np.float32)
+    x[col] = 1.0
+    np.testing.assert_array_equal(oracle.matmul_q8(q, s, x), ops_ref.dequantize_q8_0(q, s)[:, col])
+
+
+# ---- a4: threadpool tiling ------------------------------------------------------------
+
+@pytest.mark.parametrize("M,nt,tile", [(4096, 4, 1024), (100, 3, 48), (33, 8, 16), (4096, 64, 64), (1000, 7, 144)])
+def test_tile_rule(oracle, M, nt, tile):
+    # threadpool.c:408-410: round_up(ceil(M/nt), 16)
+    assert oracle.tile_rows(M, nt) == tile
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+def test_q4_mt_bitwise_independent_of_threads(oracle, variant):
+    rng = np.random.default_rng(3)
+    q, s = _rand_q4(rng, 1000, 256)
+    x = rng.standard_normal(256).astype(np.float32)
+    ref = oracle.matmul_q4(q, s, x, "avx2" if variant == 0 else "avx512")
+    for nt in (1, 2, 3, 4, 7, 8):
+        np.testing.assert_array_equal(oracle.matmul_q4_mt(q, s, x, nt, variant), ref)
+    assert oracle.threadpool_size() == 8
+
+
+def test_q8_mt_bitwise_and_small_m_fallback(oracle):
+    rng = np.random.default_rng(4)
+    q, s = _rand_q8(rng, 300, 128)
+    x = rng.standard_normal(128).astype(np.float32)
+    ref = oracle.matmul_q8(q, s, x)
+    for nt in (2, 5):
+        np.testing.assert_array_equal(oracle.matmul_q8_mt(q, s, x, nt), ref)
+    oracle.threadpool_init(3)
+    y = oracle.matmul_q8_mt(q[:31], s[:31], x, 16)  # M < 32: single thread, pool untouched
+    np.testing.assert_array_equal(y, ref[:31])
+    assert oracle.threadpool_size() == 3
+
+
+# ---- GGUF blocks, fp16, quantizers -------------------------------------------------------
+
+def test_fp16_widen_matches_numpy_everywhere(oracle):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = np.array([oracle.f16_to_f32(int(v)) for v in h[::7]], np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32)[~np.isnan(got)], ref[::7].view(np.uint32)[~np.isnan(got)])
+
+
+def test_fp16_narrow_matches_numpy(oracle):
+    rng = np.random.default_rng(6)
+    vals = np.concatenate([
+        rng.standard_normal(3000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 3000),
+        np.array([0.0, -0.0, 65504, 65519.99, 65520, 1e9, 2 ** -24, 2 ** -25, 3 * 2 ** -26, 6.1e-5], np.float32),
+    ]).astype(np.float32)
+    got = np.array([oracle.f32_to_f16(float(v)) for v in vals], np.uint16)
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_quantize_known_answers(oracle):
+    with np.load(GOLDEN_DIR / "quant_known_answers.npz") as f:
+        np.testing.assert_array_equal(oracle.quantize_q4_0(f["q4_w"]), f["q4_blocks"])
+        np.testing.assert_array_equal(oracle.quantize_q8_0(f["q8_w"]), f["q8_blocks"])
+
+
+def test_q4_gguf_equals_split_path(oracle):
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal((96, 256)) * 0.02).astype(np.float32)
+    blocks = oracle.quantize_q4_0(w)
+    qs, sc = oracle.split_q4_0(blocks)
+    x = rng.standard_normal(256).astype(np.float32)
+    np.testing.assert_array_equal(oracle.matmul_q4_0_gguf(blocks, x), oracle.matmul_q4(qs, sc, x))
+    np.testing.assert_array_equal(oracle.matmul_q4_0_gguf(blocks, x, nt=4), oracle.matmul_q4(qs, sc, x))
+    np.testing.assert_array_equal(oracle.dequantize_q4_0(blocks), ops_ref.dequantize_q4_0(qs, sc))
+
+
+def test_q8_gguf_equals_split_path(oracle):
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((64, 512)) * 0.02).astype(np.float32)
+    blocks = oracle.quantize_q8_0(w)
+    qs, sc = oracle.split_q8_0(blocks)
+    x = rng.standard_normal(512).astype(np.float32)
+    np.testing.assert_array_equal(oracle.matmul_q8_0_gguf(blocks, x), oracle.matmul_q8(qs, sc, x))
+    np.testing.assert_array_equal(oracle.dequantize_q8_0(blocks), ops_ref.dequantize_q8_0(qs, sc))
+
+
+def test_quantizers_reconstruct_within_half_step(oracle):
+    rng = np.random.default_rng(10)
+    w = (rng.standard_normal((64, 512)) * 0.02).astype(np.float32)
+    b4 = oracle.quantize_q4_0(w)
+    _, s4 = oracle.split_q4_0(b4)
+    # Q4_0 spans [-8d, 7d]: the element opposite the peak clamps from 8d to 7d,
+    # so the bound is |d| (plus the fp16 rounding of d, at most 8 |d| 2^-11).
+    err4 = np.abs(oracle.dequantize_q4_0(b4) - w).reshape(64, 16, 32).max(-1)
+    assert np.all(err4 <= np.abs(s4) * (1 + 8 * 2 ** -11) + 1e-12)
+    b8 = oracle.quantize_q8_0(w)
+    _, s8 = oracle.split_q8_0(b8)
+    # half a step, plus |q| <= 127 times the fp16 rounding of d
+    err8 = np.abs(oracle.dequantize_q8_0(b8) - w).reshape(64, 16, 32).max(-1)
+    assert np.all(err8 <= np.abs(s8) * (0.5 + 127 * 2 ** -11) + 1e-12)
+
+
+# ---- a8: GEMM recipe ---------------------------------------------------------------------
+
+def test_gemm_against_exact_integer_form(oracle):
+    rng = np.random.default_rng(12)
+    T, M, K = 5, 7, 256
+    wb = oracle.quantize_q8_0((rng.standard_normal((M, K)) * 0.02).astype(np.float32))
+    ab = oracle.quantize_q8_0(rng.standard_normal((T, K)).astype(np.float32))
+    c = oracle.gemm_q8_0(wb, ab)
+    wq, ws = oracle.split_q8_0(wb)
+    aq, as_ = oracle.split_q8_0(ab)
+    idot = np.einsum("mbj,tbj->tmb", wq.astype(np.int64), aq.astype(np.int64))
+    exact = (idot.astype(np.float64) * ws[None].astype(np.float64) * as_[:, None].astype(np.float64)).sum(-1)
+    l1 = np.abs(oracle.dequantize_q8_0(ab).astype(np.float64)) @ np.abs(oracle.dequantize_q8_0(wb).astype(np.float64)).T
+    assert np.all(np.abs(c - exact) <= 1e-6 * l1 + 1e-30)
+    np.testing.assert_array_equal(oracle.gemm_q8_0(wb, ab, nt=3), c)
+
+
+# ---- decode attention over fp16 KV -----------------------------------------------------------
+
+def test_attention_decode_f16_against_numpy(oracle):
+    rng = np.random.default_rng(13)
+    n_heads, n_kv, hd, n_pos, max_pos = 8, 2, 64, 37, 40
+    q = rng.standard_normal((n_heads, hd)).astype(np.float32)
+    kc = rng.standard_normal((max_pos, n_kv, hd)).astype(np.float16)
+    vc = rng.standard_normal((max_pos, n_kv, hd)).astype(np.float16)
+    got = oracle.attention_decode_f16(q, kc.view(np.uint16), vc.view(np.uint16), n_pos, n_kv)
+    got_mt = oracle.attention_decode_f16(q, kc.view(np.uint16), vc.view(np.uint16), n_pos, n_kv, nt=4)
+    np.testing.assert_array_equal(got, got_mt)
+    for h in range(n_heads):
+        kv = h // (n_heads // n_kv)
+        k = kc[:n_pos, kv].astype(np.float64)
+        v = vc[:n_pos, kv].astype(np.float64)
+        s = k @ q[h].astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        ref = (p / p.sum()) @ v
+        np.testing.assert_allclose(got[h], ref, rtol=0, atol=1e-6)
