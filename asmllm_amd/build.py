@@ -25,6 +25,9 @@ LIB_PATH = LIB_DIR / "libasmllm.so"
 
 SOURCES = [
     "matvec.hip",
+    "matvec_mfma.hip",
+    "decode_ops.hip",
+    "quant.hip",
     "capi.hip",
 ]
 

@@ -44,6 +44,43 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 namespace {
+struct LdsGrant {
+    const void* kernel;
+    int device;
+    size_t bytes;
+};
+std::mutex g_lds_mu;
+LdsGrant g_lds[256];
+int g_lds_n = 0;
+}  // namespace
+
+int dynamic_lds(const void* kernel, size_t bytes) {
+    if (bytes <= 64 * 1024) return kOk;
+    int dev = 0;
+    ASMHIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_lds_mu);
+    int slot = -1;
+    for (int i = 0; i < g_lds_n; ++i)
+        if (g_lds[i].kernel == kernel && g_lds[i].device == dev) {
+            if (g_lds[i].bytes >= bytes) return kOk;
+            slot = i;
+            break;
+        }
+    hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(kUnsupported, "kernel needs %zu bytes of LDS: hipFuncSetAttribute failed: %s", bytes,
+                    hipGetErrorString(e));
+    }
+    if (slot < 0) {
+        if (g_lds_n == (int)(sizeof(g_lds) / sizeof(g_lds[0]))) return kOk;  // table full: set again next time
+        slot = g_lds_n++;
+    }
+    g_lds[slot] = {kernel, dev, bytes};
+    return kOk;
+}
+
+namespace {
 
 int current_device(int* dev) {
     int n = 0;
@@ -97,14 +134,16 @@ bool is_device_pointer(const void* p) {
 struct Operand {
     const void* host;  // user pointer
     size_t bytes;
-    bool on_device;
-    void* dev;  // device address used by the kernel
+    bool in;   // uploaded before the kernel when host-resident
+    bool out;  // downloaded after the kernel when host-resident
+    bool on_device = false;
+    void* dev = nullptr;  // device address used by the kernel
 };
 
 size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Places every host operand in the staging buffer and uploads the inputs.
-int stage(DeviceState* st, Operand* ops, int n_ops, int n_inputs) {
+int stage(DeviceState* st, Operand* ops, int n_ops) {
     size_t need = 0;
     for (int i = 0; i < n_ops; ++i) {
         ops[i].on_device = is_device_pointer(ops[i].host);
@@ -122,20 +161,40 @@ int stage(DeviceState* st, Operand* ops, int n_ops, int n_inputs) {
         }
         ops[i].dev = static_cast<char*>(st->staging) + off;
         off += round256(ops[i].bytes);
-        if (i < n_inputs)
+        if (ops[i].in)
             ASMHIP_TRY(hipMemcpyAsync(ops[i].dev, ops[i].host, ops[i].bytes, hipMemcpyHostToDevice, st->stream));
     }
     return kOk;
 }
 
-// Downloads host-resident outputs (ops[first..n_ops)) and waits for the stream.
-int finish(DeviceState* st, Operand* ops, int n_ops, int first_output) {
-    for (int i = first_output; i < n_ops; ++i)
-        if (!ops[i].on_device)
+// Downloads host-resident outputs and waits for the stream.
+int finish(DeviceState* st, Operand* ops, int n_ops) {
+    for (int i = 0; i < n_ops; ++i)
+        if (ops[i].out && !ops[i].on_device)
             ASMHIP_TRY(hipMemcpyAsync(const_cast<void*>(ops[i].host), ops[i].dev, ops[i].bytes,
                                       hipMemcpyDeviceToHost, st->stream));
     ASMHIP_TRY(hipStreamSynchronize(st->stream));
     return kOk;
+}
+
+// Synchronous call: stage the operands, enqueue `launch` on the library stream
+// with their device addresses, bring the outputs back and wait.
+template <class F>
+int sync_call(Operand* ops, int n_ops, F&& launch) {
+    for (int i = 0; i < n_ops; ++i)
+        if (!ops[i].host) return fail(kInvalidArgument, "null pointer argument");
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState* st = nullptr;
+    int rc = ensure_state(&st);
+    if (rc) return rc;
+    rc = stage(st, ops, n_ops);
+    if (rc) return rc;
+    rc = launch(st->stream);
+    if (rc) {
+        (void)hipStreamSynchronize(st->stream);
+        return rc;
+    }
+    return finish(st, ops, n_ops);
 }
 
 void report(int rc, const char* fn) {
@@ -143,30 +202,20 @@ void report(int rc, const char* fn) {
 }
 
 int sync_matvec(QuantType qt, const void* q, const float* s, const float* x, float* y, int64_t M, int64_t K) {
-    if (!q || !s || !x || !y) return fail(kInvalidArgument, "null pointer argument");
     if (M <= 0 || K <= 0 || K % 32 != 0)
         return fail(kInvalidArgument, "need M > 0, K > 0 and K %% 32 == 0 (got M=%lld K=%lld)", (long long)M,
                     (long long)K);
-    std::lock_guard<std::mutex> lock(g_mu);
-    DeviceState* st = nullptr;
-    int rc = ensure_state(&st);
-    if (rc) return rc;
     const size_t nb = (size_t)(K / 32);
     Operand ops[4] = {
-        {q, (size_t)M * nb * (qt == QuantType::Q4_0 ? 16 : 32), false, nullptr},
-        {s, (size_t)M * nb * sizeof(float), false, nullptr},
-        {x, (size_t)K * sizeof(float), false, nullptr},
-        {y, (size_t)M * sizeof(float), false, nullptr},
+        {q, (size_t)M * nb * (qt == QuantType::Q4_0 ? 16 : 32), true, false},
+        {s, (size_t)M * nb * sizeof(float), true, false},
+        {x, (size_t)K * sizeof(float), true, false},
+        {y, (size_t)M * sizeof(float), false, true},
     };
-    rc = stage(st, ops, 4, 3);
-    if (rc) return rc;
-    rc = matvec_launch(qt, false, ops[0].dev, static_cast<const float*>(ops[1].dev),
-                       static_cast<const float*>(ops[2].dev), static_cast<float*>(ops[3].dev), M, K, st->stream);
-    if (rc) {
-        (void)hipStreamSynchronize(st->stream);
-        return rc;
-    }
-    return finish(st, ops, 4, 3);
+    return sync_call(ops, 4, [&](hipStream_t stream) {
+        return matvec_launch(qt, false, ops[0].dev, static_cast<const float*>(ops[1].dev),
+                             static_cast<const float*>(ops[2].dev), static_cast<float*>(ops[3].dev), M, K, stream);
+    });
 }
 
 void record_pool_size(int n) {
@@ -262,6 +311,80 @@ extern "C" void asm_threadpool_dispatch_q8(const int8_t* qweights, const float* 
     report(sync_matvec(QuantType::Q8_0, qweights, scales, x, y, M, K), "asm_threadpool_dispatch_q8");
 }
 
+// rmsnorm_avx2.asm:63-151: y = (x * (1/sqrt(mean(x^2) + eps))) * w.
+extern "C" void asm_rmsnorm(const float* x, const float* w, float* y, int64_t dim, float eps) {
+    if (dim <= 0) return report(fail(kInvalidArgument, "dim must be > 0"), "asm_rmsnorm");
+    const size_t b = (size_t)dim * sizeof(float);
+    Operand ops[3] = {{x, b, true, false}, {w, b, true, false}, {y, b, false, true}};
+    report(sync_call(ops, 3,
+                     [&](hipStream_t st) {
+                         return rmsnorm_launch((const float*)ops[0].dev, (const float*)ops[1].dev,
+                                               (float*)ops[2].dev, dim, eps, st);
+                     }),
+           "asm_rmsnorm");
+}
+
+// rope_avx2.asm:52-146: one head of q and one of k, rotated in place.
+extern "C" void asm_rope(float* q, float* k, int64_t head_dim, int64_t pos, float theta) {
+    if (head_dim <= 0) return report(fail(kInvalidArgument, "head_dim must be > 0"), "asm_rope");
+    const size_t b = (size_t)head_dim * sizeof(float);
+    Operand ops[2] = {{q, b, true, true}, {k, b, true, true}};
+    report(sync_call(ops, 2,
+                     [&](hipStream_t st) {
+                         return rope_launch((float*)ops[0].dev, (float*)ops[1].dev, 1, 1, head_dim, nullptr, pos,
+                                            theta, st);
+                     }),
+           "asm_rope");
+}
+
+// softmax_avx2.asm:48-130; x == y allowed.
+extern "C" void asm_softmax(const float* x, float* y, int64_t dim) {
+    if (dim <= 0) return report(fail(kInvalidArgument, "dim must be > 0"), "asm_softmax");
+    const size_t b = (size_t)dim * sizeof(float);
+    if (x == y) {
+        Operand ops[1] = {{y, b, true, true}};
+        return report(sync_call(ops, 1,
+                                [&](hipStream_t st) {
+                                    return softmax_launch((const float*)ops[0].dev, (float*)ops[0].dev, dim, st);
+                                }),
+                      "asm_softmax");
+    }
+    Operand ops[2] = {{x, b, true, false}, {y, b, false, true}};
+    report(sync_call(ops, 2,
+                     [&](hipStream_t st) {
+                         return softmax_launch((const float*)ops[0].dev, (float*)ops[1].dev, dim, st);
+                     }),
+           "asm_softmax");
+}
+
+// swiglu_avx2.asm:45-81: gate = gate / (1 + exp(-gate)) * up, in place.
+extern "C" void asm_silu_hadamard(float* gate, const float* up, int64_t dim) {
+    if (dim <= 0) return report(fail(kInvalidArgument, "dim must be > 0"), "asm_silu_hadamard");
+    const size_t b = (size_t)dim * sizeof(float);
+    Operand ops[2] = {{gate, b, true, true}, {up, b, true, false}};
+    report(sync_call(ops, 2,
+                     [&](hipStream_t st) {
+                         return silu_launch((float*)ops[0].dev, (const float*)ops[1].dev, dim, st);
+                     }),
+           "asm_silu_hadamard");
+}
+
+// attention_avx2.asm:59-218: y = softmax(q k^T * scale) v over [seq][head_dim] rows.
+extern "C" void asm_attention(const float* q, const float* k, const float* v, float* y, int64_t seq_len,
+                              int64_t head_dim, float scale) {
+    if (seq_len <= 0 || head_dim <= 0)
+        return report(fail(kInvalidArgument, "need seq_len > 0 and head_dim > 0"), "asm_attention");
+    const size_t b = (size_t)seq_len * head_dim * sizeof(float);
+    Operand ops[4] = {{q, b, true, false}, {k, b, true, false}, {v, b, true, false}, {y, b, false, true}};
+    report(sync_call(ops, 4,
+                     [&](hipStream_t st) {
+                         return attention_launch((const float*)ops[0].dev, (const float*)ops[1].dev,
+                                                 (const float*)ops[2].dev, (float*)ops[3].dev, seq_len, head_dim,
+                                                 scale, st);
+                     }),
+           "asm_attention");
+}
+
 // ---- device entry points -------------------------------------------------------
 
 static int check_ptrs(const void* a, const void* b, const void* c) {
@@ -301,6 +424,117 @@ extern "C" int asmhip_dequantize_q4_0(const void* blocks, float* w, int64_t rows
 extern "C" int asmhip_dequantize_q8_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream) {
     if (!blocks || !w) return fail(kInvalidArgument, "null pointer argument");
     return dequant_launch(QuantType::Q8_0, blocks, w, rows, K, (hipStream_t)stream);
+}
+
+static int quant_type(int qtype, QuantType* qt) {
+    if (qtype == ASMHIP_Q4_0) *qt = QuantType::Q4_0;
+    else if (qtype == ASMHIP_Q8_0) *qt = QuantType::Q8_0;
+    else return fail(kInvalidArgument, "unknown quantization type %d", qtype);
+    return kOk;
+}
+
+extern "C" int asmhip_matmul_fused(int qtype, const void* blocks, const float* x, float* y, int64_t M, int64_t K,
+                                   int pre_op, const float* pre_arg, float eps, int accumulate, void* stream) {
+    QuantType qt;
+    int rc = check_ptrs(blocks, x, y);
+    if (!rc) rc = quant_type(qtype, &qt);
+    if (rc) return rc;
+    MatvecOpts o;
+    o.pre = pre_op;
+    o.pre_arg = pre_arg;
+    o.eps = eps;
+    o.accumulate = accumulate != 0;
+    return matvec_launch(qt, true, blocks, nullptr, x, y, M, K, (hipStream_t)stream, o);
+}
+
+extern "C" int asmhip_set_q4_kernel(int kernel) { return set_q4_kernel(kernel); }
+extern "C" int asmhip_get_q4_kernel(void) { return get_q4_kernel(); }
+
+extern "C" int asmhip_quantize(int qtype, const float* w, void* blocks, int64_t rows, int64_t K, void* stream) {
+    QuantType qt;
+    if (!w || !blocks) return fail(kInvalidArgument, "null pointer argument");
+    int rc = quant_type(qtype, &qt);
+    return rc ? rc : quantize_launch(qt, w, blocks, rows, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_random_blocks(int qtype, void* blocks, int64_t rows, int64_t K, uint64_t seed, float stddev,
+                                    void* stream) {
+    QuantType qt;
+    if (!blocks) return fail(kInvalidArgument, "null pointer argument");
+    int rc = quant_type(qtype, &qt);
+    return rc ? rc : random_blocks_launch(qt, blocks, rows, K, seed, stddev, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_random_f16(void* out, int64_t n, uint64_t seed, float stddev, void* stream) {
+    if (!out) return fail(kInvalidArgument, "null pointer argument");
+    return random_f16_launch(out, n, seed, stddev, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_fill_f32(float* out, int64_t n, float value, void* stream) {
+    if (!out) return fail(kInvalidArgument, "null pointer argument");
+    return fill_f32_launch(out, n, value, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_rmsnorm(const float* x, const float* w, float* y, int64_t dim, float eps, void* stream) {
+    int rc = check_ptrs(x, w, y);
+    return rc ? rc : rmsnorm_launch(x, w, y, dim, eps, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_rope(float* q, float* k, int64_t n_q_heads, int64_t n_k_heads, int64_t head_dim,
+                           const int* pos_dev, int64_t pos, float theta, void* stream) {
+    if ((n_q_heads && !q) || (n_k_heads && !k)) return fail(kInvalidArgument, "null pointer argument");
+    return rope_launch(q, k, n_q_heads, n_k_heads, head_dim, pos_dev, pos, theta, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_softmax(const float* x, float* y, int64_t dim, void* stream) {
+    if (!x || !y) return fail(kInvalidArgument, "null pointer argument");
+    return softmax_launch(x, y, dim, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_silu_hadamard(float* gate, const float* up, int64_t dim, void* stream) {
+    if (!gate || !up) return fail(kInvalidArgument, "null pointer argument");
+    return silu_launch(gate, up, dim, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_attention(const float* q, const float* k, const float* v, float* y, int64_t seq_len,
+                                int64_t head_dim, float scale, void* stream) {
+    if (!q || !k || !v || !y) return fail(kInvalidArgument, "null pointer argument");
+    return attention_launch(q, k, v, y, seq_len, head_dim, scale, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_rope_kv_write(float* qkv, void* k_cache, void* v_cache, int n_heads, int n_kv_heads,
+                                    int head_dim, const int* pos_dev, int max_ctx, float theta, void* stream) {
+    if (!qkv || !k_cache || !v_cache || !pos_dev) return fail(kInvalidArgument, "null pointer argument");
+    if (n_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return fail(kInvalidArgument, "bad attention shape");
+    return rope_kv_write_launch(qkv, k_cache, v_cache, n_heads, n_kv_heads, head_dim, pos_dev, max_ctx, theta,
+                                (hipStream_t)stream);
+}
+
+extern "C" int64_t asmhip_attention_decode_workspace(int n_heads, int head_dim, int max_ctx) {
+    if (n_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return 0;
+    return (int64_t)n_heads * attn_decode_splits(max_ctx) * (head_dim + 2);
+}
+
+extern "C" int asmhip_attention_decode(const float* q, const void* k_cache, const void* v_cache, float* workspace,
+                                       float* out, int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
+                                       int max_ctx, void* stream) {
+    if (!q || !k_cache || !v_cache || !workspace || !out || !pos_dev)
+        return fail(kInvalidArgument, "null pointer argument");
+    if (n_heads <= 0 || max_ctx <= 0) return fail(kInvalidArgument, "bad attention shape");
+    return attn_decode_launch(q, k_cache, v_cache, workspace, out, n_heads, n_kv_heads, head_dim, pos_dev, max_ctx,
+                              (hipStream_t)stream);
+}
+
+extern "C" int asmhip_embed_q4_0(const void* table, const int* token_dev, float* x, int n_vocab, int dim,
+                                 void* stream) {
+    if (!table || !token_dev || !x) return fail(kInvalidArgument, "null pointer argument");
+    if (n_vocab <= 0 || dim <= 0) return fail(kInvalidArgument, "bad embedding shape");
+    return embed_q4_0_launch(table, token_dev, x, n_vocab, dim, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_argmax(const float* logits, int n, int* token_dev, int* pos_dev, void* stream) {
+    if (!logits || !token_dev) return fail(kInvalidArgument, "null pointer argument");
+    return argmax_launch(logits, n, token_dev, pos_dev, (hipStream_t)stream);
 }
 
 // ---- plumbing --------------------------------------------------------------------

@@ -20,6 +20,11 @@ enum Status : int {
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_fail(hipError_t e, const char* what);
 
+// Raises `kernel`'s dynamic-LDS limit to at least `bytes` on the current
+// device (launches above 64 KB need it).  Granted sizes are cached per kernel
+// and device, so the hot path pays one lookup.
+int dynamic_lds(const void* kernel, size_t bytes);
+
 #define ASMHIP_TRY(expr)                                   \
     do {                                                   \
         hipError_t _e = (expr);                            \

@@ -1,0 +1,445 @@
+// Decode-step kernels for gfx950: the ops asmllm's forward_token sequences
+// around the matvecs (src/runtime/generate.py:261-326), so a whole token
+// step stays on the GPU.
+//
+//   rmsnorm        rmsnorm_avx2.asm:63-151       y = (x * (1/sqrt(mean(x^2) + eps))) * w
+//   rope           rope_avx2.asm:52-146          interleaved pairs (2p, 2p+1), freq = theta^(-2p/hd)
+//   softmax        softmax_avx2.asm:48-130       max, exp(x - max), / sum
+//   silu_hadamard  swiglu_avx2.asm:45-81         gate = gate / (1 + exp(-gate)) * up
+//   attention      attention_avx2.asm:59-218     softmax(q k^T * scale) v, all rows (non-causal)
+//
+// plus the device-side pieces of the decode engine: RoPE fused with the fp16
+// KV-cache write, split-K attention over the fp16 cache, embedding-row
+// dequantization and greedy argmax.  The angle of RoPE is formed in double
+// precision: the reference forms it in x87 extended precision, and at decode
+// positions in the thousands an fp32 angle would be off by ~1e-4 rad.
+#include <math.h>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace asmhip {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+template <int kThreads>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kThreads / kWave; ++i) t += red[i];
+    return t;
+}
+
+template <int kThreads>
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int i = 1; i < kThreads / kWave; ++i) t = fmaxf(t, red[i]);
+    return t;
+}
+
+// ---- rmsnorm: one workgroup per vector -----------------------------------------
+__global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                       float* __restrict__ y, int dim, float eps) {
+    __shared__ float red[16];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < dim; i += 1024) s = fmaf(x[i], x[i], s);
+    s = block_sum<1024>(s, red);
+    const float inv = 1.0f / sqrtf(s / (float)dim + eps);
+    for (int i = threadIdx.x; i < dim; i += 1024) y[i] = __fmul_rn(__fmul_rn(x[i], inv), w[i]);
+}
+
+// ---- rope: pair (2p, 2p+1) of every head of q and of k -----------------------------
+__device__ __forceinline__ void rope_angle(int p, int hd, int pos, float theta, float* c, float* s) {
+    const float e = (float)(-2 * p) / (float)hd;  // divss in the reference
+    const double ang = pow((double)theta, (double)e) * (double)(float)pos;
+    *c = (float)cos(ang);
+    *s = (float)sin(ang);
+}
+
+__device__ __forceinline__ void rotate(float* v, float c, float s) {
+    const float a = v[0], b = v[1];
+    v[0] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
+    v[1] = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+}
+
+__global__ __launch_bounds__(kBlock) void rope_kernel(float* __restrict__ q, float* __restrict__ k, int n_q_heads,
+                                                      int n_k_heads, int hd, const int* __restrict__ pos_ptr,
+                                                      int pos, float theta) {
+    const int half = hd >> 1;
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    const int total = (n_q_heads + n_k_heads) * half;
+    if (i >= total) return;
+    const int p = i % half, head = i / half;
+    const int position = pos_ptr ? *pos_ptr : pos;
+    float c, s;
+    rope_angle(p, hd, position, theta, &c, &s);
+    float* v = head < n_q_heads ? q + (size_t)head * hd : k + (size_t)(head - n_q_heads) * hd;
+    rotate(v + 2 * p, c, s);
+}
+
+// ---- RoPE on q/k of a fused qkv vector + fp16 KV-cache write at *pos --------------
+// qkv = [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)]; caches are head-major
+// [n_kv][max_ctx][hd] fp16.  q is rotated in place.
+__global__ __launch_bounds__(kBlock) void rope_kv_write_kernel(float* __restrict__ qkv, __half* __restrict__ kc,
+                                                               __half* __restrict__ vc, int n_heads, int n_kv, int hd,
+                                                               const int* __restrict__ pos_ptr, int max_ctx,
+                                                               float theta) {
+    const int half = hd >> 1;
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    const int n_pairs = (n_heads + n_kv) * half;
+    const int pos = *pos_ptr;
+    if (pos < 0 || pos >= max_ctx) return;  // the host never lets this happen; no write out of range
+    if (i < n_pairs) {
+        const int p = i % half, head = i / half;
+        float c, s;
+        rope_angle(p, hd, pos, theta, &c, &s);
+        float v[2] = {qkv[(size_t)head * hd + 2 * p], qkv[(size_t)head * hd + 2 * p + 1]};
+        rotate(v, c, s);
+        if (head < n_heads) {
+            qkv[(size_t)head * hd + 2 * p] = v[0];
+            qkv[(size_t)head * hd + 2 * p + 1] = v[1];
+        } else {
+            const int kh = head - n_heads;
+            __half* dst = kc + ((size_t)kh * max_ctx + pos) * hd + 2 * p;
+            dst[0] = __float2half_rn(v[0]);
+            dst[1] = __float2half_rn(v[1]);
+        }
+    } else if (i < n_pairs + n_kv * hd) {
+        const int j = i - n_pairs, kh = j / hd, d = j % hd;
+        vc[((size_t)kh * max_ctx + pos) * hd + d] = __float2half_rn(qkv[(size_t)(n_heads + n_kv) * hd + j]);
+    }
+}
+
+// ---- softmax of one vector (x == y allowed) -------------------------------------------
+__global__ __launch_bounds__(1024) void softmax_kernel(const float* x, float* y, int dim) {
+    __shared__ float red[16];
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < dim; i += 1024) m = fmaxf(m, x[i]);
+    m = block_max<1024>(m, red);
+    float s = 0.f;
+    for (int i = threadIdx.x; i < dim; i += 1024) {
+        const float e = expf(x[i] - m);
+        y[i] = e;
+        s += e;
+    }
+    s = block_sum<1024>(s, red);
+    for (int i = threadIdx.x; i < dim; i += 1024) y[i] = y[i] / s;
+}
+
+// ---- silu(gate) * up, in place on gate ----------------------------------------------
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return __fmul_rn(g / (1.0f + expf(-g)), u);
+}
+
+__global__ __launch_bounds__(kBlock) void silu_kernel(float* __restrict__ g, const float* __restrict__ u, int dim) {
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i < dim) g[i] = silu_mul(g[i], u[i]);
+}
+
+// ---- reference attention: one workgroup per query row, scores in LDS ----------------
+__global__ __launch_bounds__(kBlock) void attention_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                           const float* __restrict__ v, float* __restrict__ y,
+                                                           int seq, int hd, float scale) {
+    extern __shared__ float sc[];  // seq scores
+    __shared__ float red[kBlock / kWave];
+    const int row = blockIdx.x;
+    const float* qi = q + (size_t)row * hd;
+    for (int j = threadIdx.x; j < seq; j += kBlock) {
+        const float* kj = k + (size_t)j * hd;
+        float d = 0.f;
+        for (int t = 0; t < hd; ++t) d = fmaf(qi[t], kj[t], d);
+        sc[j] = d * scale;
+    }
+    __syncthreads();
+    float m = -INFINITY;
+    for (int j = threadIdx.x; j < seq; j += kBlock) m = fmaxf(m, sc[j]);
+    m = block_max<kBlock>(m, red);
+    float s = 0.f;
+    for (int j = threadIdx.x; j < seq; j += kBlock) {
+        const float e = expf(sc[j] - m);
+        sc[j] = e;
+        s += e;
+    }
+    s = block_sum<kBlock>(s, red);
+    __syncthreads();
+    for (int t = threadIdx.x; t < hd; t += kBlock) {
+        float a = 0.f;
+        for (int j = 0; j < seq; ++j) a = fmaf(sc[j], v[(size_t)j * hd + t], a);
+        y[(size_t)row * hd + t] = a / s;
+    }
+}
+
+// ---- decode attention over the fp16 cache, split over positions ---------------------
+// grid (n_heads, n_splits); workgroup = 4 waves; kSlots positions in flight per
+// workgroup, HD/8 lanes per position each holding 8 dimensions (16 bytes).
+// Partial result per (head, split): [m, l, acc[HD]] with acc unnormalized.
+template <int HD>
+__global__ __launch_bounds__(kBlock) void attn_decode_partial(const float* __restrict__ q,
+                                                              const __half* __restrict__ kc,
+                                                              const __half* __restrict__ vc,
+                                                              float* __restrict__ part, int n_heads, int n_kv,
+                                                              const int* __restrict__ pos_ptr, int max_ctx,
+                                                              int split_len) {
+    constexpr int kLanesPerPos = HD / 8;
+    constexpr int kSlots = kBlock / kLanesPerPos;
+    __shared__ float sc[1024];
+    __shared__ float red[kBlock / kWave];
+    __shared__ float accs[kSlots][HD + 1];
+    const int h = blockIdx.x, split = blockIdx.y;
+    const int kvh = h / (n_heads / n_kv);
+    const int n_pos = min(*pos_ptr + 1, max_ctx);
+    const int p0 = split * split_len, p1 = min(p0 + split_len, n_pos);
+    float* out = part + ((size_t)h * gridDim.y + split) * (HD + 2);
+    if (p0 >= p1) {
+        if (threadIdx.x == 0) {
+            out[0] = -INFINITY;
+            out[1] = 0.f;
+        }
+        for (int d = threadIdx.x; d < HD; d += kBlock) out[2 + d] = 0.f;
+        return;
+    }
+    const int slot = threadIdx.x / kLanesPerPos, c = threadIdx.x % kLanesPerPos;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float qv[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) qv[t] = q[(size_t)h * HD + 8 * c + t] * scale;
+    const __half* kbase = kc + (size_t)kvh * max_ctx * HD;
+    const __half* vbase = vc + (size_t)kvh * max_ctx * HD;
+
+    // pass 1: scores
+    for (int p = p0 + slot; p < p1; p += kSlots) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(kbase + (size_t)p * HD + 8 * c);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+        float d = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            d = fmaf(qv[2 * t], half_lo(w[t]), d);
+            d = fmaf(qv[2 * t + 1], half_hi(w[t]), d);
+        }
+#pragma unroll
+        for (int o = kLanesPerPos / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, kWave);
+        if (c == 0) sc[p - p0] = d;
+    }
+    __syncthreads();
+    const int n = p1 - p0;
+    float m = -INFINITY;
+    for (int j = threadIdx.x; j < n; j += kBlock) m = fmaxf(m, sc[j]);
+    m = block_max<kBlock>(m, red);
+    float l = 0.f;
+    for (int j = threadIdx.x; j < n; j += kBlock) {
+        const float e = expf(sc[j] - m);
+        sc[j] = e;
+        l += e;
+    }
+    l = block_sum<kBlock>(l, red);
+    __syncthreads();
+
+    // pass 2: p . V
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int p = p0 + slot; p < p1; p += kSlots) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(vbase + (size_t)p * HD + 8 * c);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+        const float pr = sc[p - p0];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            acc[2 * t] = fmaf(pr, half_lo(w[t]), acc[2 * t]);
+            acc[2 * t + 1] = fmaf(pr, half_hi(w[t]), acc[2 * t + 1]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) accs[slot][8 * c + t] = acc[t];
+    __syncthreads();
+    for (int d = threadIdx.x; d < HD; d += kBlock) {
+        float a = 0.f;
+        for (int sl = 0; sl < kSlots; ++sl) a += accs[sl][d];
+        out[2 + d] = a;
+    }
+    if (threadIdx.x == 0) {
+        out[0] = m;
+        out[1] = l;
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_decode_combine(const float* __restrict__ part, float* __restrict__ out,
+                                                          int n_splits) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float* ph = part + (size_t)h * n_splits * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ph[(size_t)s * (HD + 2)]);
+    float L = 0.f, a = 0.f;
+    for (int s = 0; s < n_splits; ++s) {
+        const float* e = ph + (size_t)s * (HD + 2);
+        if (e[0] == -INFINITY) continue;
+        const float f = expf(e[0] - M);
+        L = fmaf(e[1], f, L);
+        a = fmaf(e[2 + d], f, a);
+    }
+    out[(size_t)h * HD + d] = a / L;
+}
+
+// ---- embedding row of a Q4_0 table -----------------------------------------------------
+__global__ __launch_bounds__(kBlock) void embed_q4_0_kernel(const uint8_t* __restrict__ table,
+                                                            const int* __restrict__ token, float* __restrict__ x,
+                                                            int n_vocab, int dim) {
+    const int t = *token;
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= dim || t < 0 || t >= n_vocab) return;
+    const int nb = dim / 32, b = i / 32, j = i % 32;
+    const uint8_t* blk = table + ((size_t)t * nb + b) * 18;
+    const float d = __half2float(__ushort_as_half((unsigned short)(blk[0] | (blk[1] << 8))));
+    const int n = j < 16 ? (blk[2 + j] & 15) : (blk[2 + j - 16] >> 4);
+    x[i] = ((float)n - 8.0f) * d;
+}
+
+// ---- greedy argmax (first index of the maximum, as numpy.argmax) -------------------------
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
+                                                      int* __restrict__ token, int* __restrict__ pos) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float x = logits[i];
+        if (x > v) {
+            v = x;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(v, o, kWave);
+        const int oi = __shfl_xor(idx, o, kWave);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) {
+        bv[w] = v;
+        bi[w] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float best = bv[0];
+        int bidx = bi[0];
+        for (int i = 1; i < 16; ++i)
+            if (bv[i] > best || (bv[i] == best && bi[i] < bidx)) {
+                best = bv[i];
+                bidx = bi[i];
+            }
+        *token = bidx;
+        if (pos) *pos = *pos + 1;
+    }
+}
+
+}  // namespace
+
+int rmsnorm_launch(const float* x, const float* w, float* y, int64_t dim, float eps, hipStream_t st) {
+    if (dim <= 0 || dim > INT32_MAX) return fail(kInvalidArgument, "rmsnorm: bad dim %lld", (long long)dim);
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, st, x, w, y, (int)dim, eps);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int rope_launch(float* q, float* k, int64_t n_q_heads, int64_t n_k_heads, int64_t hd, const int* pos_ptr,
+                int64_t pos, float theta, hipStream_t st) {
+    if (hd <= 0 || hd % 2 || n_q_heads < 0 || n_k_heads < 0 || pos < 0 || pos > INT32_MAX)
+        return fail(kInvalidArgument, "rope: need even head_dim > 0 and pos >= 0");
+    const int64_t total = (n_q_heads + n_k_heads) * (hd / 2);
+    if (total == 0) return kOk;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, st, q, k,
+                       (int)n_q_heads, (int)n_k_heads, (int)hd, pos_ptr, (int)pos, theta);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int rope_kv_write_launch(float* qkv, void* k_cache, void* v_cache, int n_heads, int n_kv, int hd,
+                         const int* pos_ptr, int max_ctx, float theta, hipStream_t st) {
+    if (hd % 2 || n_kv <= 0 || n_heads % n_kv) return fail(kInvalidArgument, "rope_kv_write: bad head layout");
+    const int total = (n_heads + n_kv) * (hd / 2) + n_kv * hd;
+    hipLaunchKernelGGL(rope_kv_write_kernel, dim3((total + kBlock - 1) / kBlock), dim3(kBlock), 0, st, qkv,
+                       (__half*)k_cache, (__half*)v_cache, n_heads, n_kv, hd, pos_ptr, max_ctx, theta);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int softmax_launch(const float* x, float* y, int64_t dim, hipStream_t st) {
+    if (dim <= 0 || dim > INT32_MAX) return fail(kInvalidArgument, "softmax: bad dim");
+    hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(1024), 0, st, x, y, (int)dim);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int silu_launch(float* g, const float* u, int64_t dim, hipStream_t st) {
+    if (dim <= 0 || dim > INT32_MAX) return fail(kInvalidArgument, "silu_hadamard: bad dim");
+    hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((dim + kBlock - 1) / kBlock)), dim3(kBlock), 0, st, g, u,
+                       (int)dim);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int attention_launch(const float* q, const float* k, const float* v, float* y, int64_t seq, int64_t hd, float scale,
+                     hipStream_t st) {
+    if (seq <= 0 || hd <= 0) return fail(kInvalidArgument, "attention: need seq > 0 and head_dim > 0");
+    if (seq > 40000) return fail(kUnsupported, "attention: seq_len %lld exceeds the LDS score buffer", (long long)seq);
+    const int rc = dynamic_lds((const void*)attention_kernel, (size_t)seq * sizeof(float));
+    if (rc) return rc;
+    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)seq), dim3(kBlock), (size_t)seq * sizeof(float), st, q, k,
+                       v, y, (int)seq, (int)hd, scale);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int attn_decode_splits(int max_ctx) { return (max_ctx + kAttnSplitLen - 1) / kAttnSplitLen; }
+
+int attn_decode_launch(const float* q, const void* k_cache, const void* v_cache, float* part, float* out,
+                       int n_heads, int n_kv, int hd, const int* pos_ptr, int max_ctx, hipStream_t st) {
+    if (n_kv <= 0 || n_heads % n_kv) return fail(kInvalidArgument, "attention: n_heads %% n_kv_heads != 0");
+    const int splits = attn_decode_splits(max_ctx);
+    dim3 grid(n_heads, splits);
+    if (hd == 128) {
+        hipLaunchKernelGGL((attn_decode_partial<128>), grid, dim3(kBlock), 0, st, q, (const __half*)k_cache,
+                           (const __half*)v_cache, part, n_heads, n_kv, pos_ptr, max_ctx, kAttnSplitLen);
+        hipLaunchKernelGGL((attn_decode_combine<128>), dim3(n_heads), dim3(128), 0, st, part, out, splits);
+    } else if (hd == 64) {
+        hipLaunchKernelGGL((attn_decode_partial<64>), grid, dim3(kBlock), 0, st, q, (const __half*)k_cache,
+                           (const __half*)v_cache, part, n_heads, n_kv, pos_ptr, max_ctx, kAttnSplitLen);
+        hipLaunchKernelGGL((attn_decode_combine<64>), dim3(n_heads), dim3(64), 0, st, part, out, splits);
+    } else {
+        return fail(kUnsupported, "attention: head_dim %d (supported: 64, 128)", hd);
+    }
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int embed_q4_0_launch(const void* table, const int* token, float* x, int n_vocab, int dim, hipStream_t st) {
+    if (dim % 32) return fail(kInvalidArgument, "embedding: dim %% 32 != 0");
+    hipLaunchKernelGGL(embed_q4_0_kernel, dim3((dim + kBlock - 1) / kBlock), dim3(kBlock), 0, st,
+                       (const uint8_t*)table, token, x, n_vocab, dim);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st) {
+    if (n <= 0) return fail(kInvalidArgument, "argmax: empty input");
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, logits, n, token, pos);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+}  // namespace asmhip

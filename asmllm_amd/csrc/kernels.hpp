@@ -10,12 +10,69 @@ namespace asmhip {
 
 enum class QuantType { Q4_0, Q8_0 };
 
+// Work fused into a matvec: a transform applied to x while it is staged, and
+// whether y is overwritten or accumulated into.
+enum PreOp : int {
+    kPreNone = 0,
+    kPreRmsNorm = 1,  // x <- (x * 1/sqrt(mean(x^2) + eps)) * arg[k]
+    kPreSwiGlu = 2,   // x <- x / (1 + exp(-x)) * arg[k]
+};
+
+struct MatvecOpts {
+    int pre = kPreNone;
+    const float* pre_arg = nullptr;
+    float eps = 0.f;
+    bool accumulate = false;  // y += W x
+};
+
 // y = W x.  gguf: W is [M][K/32] GGUF blocks; otherwise W is the split qs
 // array and `scales` the fp32 [M][K/32] scales.
 int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, const float* x, float* y,
-                  int64_t M, int64_t K, hipStream_t stream);
+                  int64_t M, int64_t K, hipStream_t stream, const MatvecOpts& opts = MatvecOpts());
+
+// Q4_0 GGUF matvec on the int8 matrix cores (matvec_launch picks it when
+// q4_0_mfma_eligible holds: K % 256 == 0, K <= 16384, 16-byte aligned x).
+// Process-wide choice of the Q4_0 GGUF kernel: auto (MFMA when eligible), the
+// fp32 VALU kernel only, or the MFMA kernel only (ineligible shapes fail).
+enum Q4Kernel : int { kQ4KernelAuto = 0, kQ4KernelFp32 = 1, kQ4KernelMfma = 2 };
+int set_q4_kernel(int kernel);
+int get_q4_kernel();
+
+bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& opts, int64_t M, int64_t K);
+int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t stream,
+                     const MatvecOpts& opts);
 
 // Exact fp32 dequantization of GGUF blocks, row-major [rows][K].
 int dequant_launch(QuantType qt, const void* w, float* out, int64_t rows, int64_t K, hipStream_t stream);
+
+// fp32 [rows][K] -> GGUF blocks (the rules of the host quantizers, bit for bit).
+int quantize_launch(QuantType qt, const float* w, void* blocks, int64_t rows, int64_t K, hipStream_t stream);
+// Q4_0 / Q8_0 blocks of N(0, stddev^2) weights from a counter-based generator.
+int random_blocks_launch(QuantType qt, void* blocks, int64_t rows, int64_t K, uint64_t seed, float stddev,
+                         hipStream_t stream);
+int random_f16_launch(void* out, int64_t n, uint64_t seed, float stddev, hipStream_t stream);
+int fill_f32_launch(float* out, int64_t n, float value, hipStream_t stream);
+
+// Decode-step ops.
+int rmsnorm_launch(const float* x, const float* w, float* y, int64_t dim, float eps, hipStream_t st);
+int rope_launch(float* q, float* k, int64_t n_q_heads, int64_t n_k_heads, int64_t hd, const int* pos_ptr,
+                int64_t pos, float theta, hipStream_t st);
+int rope_kv_write_launch(float* qkv, void* k_cache, void* v_cache, int n_heads, int n_kv, int hd,
+                         const int* pos_ptr, int max_ctx, float theta, hipStream_t st);
+int softmax_launch(const float* x, float* y, int64_t dim, hipStream_t st);
+int silu_launch(float* g, const float* u, int64_t dim, hipStream_t st);
+int attention_launch(const float* q, const float* k, const float* v, float* y, int64_t seq, int64_t hd, float scale,
+                     hipStream_t st);
+
+// Decode attention over head-major fp16 caches [n_kv][max_ctx][hd], positions
+// 0..*pos_ptr; split into kAttnSplitLen-position chunks, combined in a second
+// kernel.  `part` holds n_heads * attn_decode_splits(max_ctx) * (hd + 2) floats.
+constexpr int kAttnSplitLen = 128;
+int attn_decode_splits(int max_ctx);
+int attn_decode_launch(const float* q, const void* k_cache, const void* v_cache, float* part, float* out,
+                       int n_heads, int n_kv, int hd, const int* pos_ptr, int max_ctx, hipStream_t st);
+
+int embed_q4_0_launch(const void* table, const int* token, float* x, int n_vocab, int dim, hipStream_t st);
+int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st);
 
 }  // namespace asmhip

@@ -1,6 +1,6 @@
 // Q4_0 / Q8_0 matrix-vector kernels for gfx950.
 //
-// y[m] = sum_b d[m,b] * sum_j (q[m,b,j] - bias) * x[32b + j]
+// y[m] = sum_b d[m,b] * sum_j (q[m,b,j] - z) * x[32b + j],  z = 8 for Q4_0 and 0 for Q8_0
 //
 // Replaces the reference's asm_matmul_q4 (src/kernels/x86_64/matmul_q4_avx2.asm:57-287)
 // and asm_matmul_q8 (src/kernels/x86_64/matmul_q8_avx2.asm:51-194).  Two weight
@@ -18,13 +18,18 @@
 //   * a wave walks R rows at a time through every chunk, the x values of its
 //     pair sit in registers and are reused for all R rows;
 //   * x is staged once per workgroup in LDS (padded 4 floats per 64 so the
-//     per-lane 256 B reads are bank-conflict free), together with the per-block
-//     sum of x, which turns sum (q - 8) x into sum q x - 8 sum x;
-//   * nibbles become floats with one v_cvt_f32_ubyte{k} each: low nibbles via
-//     v & 0x0F0F0F0F, high nibbles via v & 0xF0F0F0F0 (= 16 q) against x / 16,
-//     both exact;
+//     per-lane 256 B reads are bank-conflict free); for Q4 it is stored as
+//     x / 16 (exact);
+//   * every weight becomes an exact float with one v_cvt_f32_i32 (SDWA byte
+//     select, sign extended): a Q4 nibble n is moved to the top of its byte
+//     with bit 7 flipped, which reads as the signed byte 16 (n - 8)
+//     (one v_bitop3_b32 for high nibbles, a shift plus one for low nibbles),
+//     and 16 (n - 8) * (x / 16) is exactly the reference's (n - 8) * x;
+//     Q8 bytes are converted directly;
 //   * each lane keeps one fp32 accumulator per row, reduced across the wave
 //     at the end.
+#include <atomic>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -44,50 +49,55 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     return v;
 }
 
+__device__ __forceinline__ float sbyte(uint32_t v, int k) { return (float)(int)(int8_t)((v >> (8 * k)) & 0xFFu); }
+
 // Low/high nibbles of bytes [k0, k1) of v are weights jb.. and jb+16.. of a
-// Q4 block; xl holds x[j], xh holds x[16 + j] / 16.
+// Q4 block; xl holds x[j] / 16, xh holds x[16 + j] / 16.
 template <int k0, int k1, int jb>
 __device__ __forceinline__ float q4_bytes(uint32_t v, const float* xl, const float* xh, float t) {
-    const uint32_t lo = opaque(v & 0x0F0F0F0Fu);
-    const uint32_t hi = opaque(v & 0xF0F0F0F0u);
+    const uint32_t lo = opaque(((v << 4) ^ 0x80808080u) & 0xF0F0F0F0u);  // bytes 16 (n_lo - 8)
+    const uint32_t hi = opaque((v ^ 0x80808080u) & 0xF0F0F0F0u);         // bytes 16 (n_hi - 8)
 #pragma unroll
     for (int k = k0; k < k1; ++k) {
-        t = fmaf((float)((lo >> (8 * k)) & 0xFFu), xl[jb + k - k0], t);
-        t = fmaf((float)((hi >> (8 * k)) & 0xFFu), xh[jb + k - k0], t);
+        t = fmaf(sbyte(lo, k), xl[jb + k - k0], t);
+        t = fmaf(sbyte(hi, k), xh[jb + k - k0], t);
     }
     return t;
 }
 
-// Signed bytes [k0, k1) of v (biased by +128 through the xor) times x[jb..].
+// Signed bytes [k0, k1) of v times x[jb..].
 template <int k0, int k1, int jb>
 __device__ __forceinline__ float q8_bytes(uint32_t v, const float* xv, float t) {
-    const uint32_t u = opaque(v ^ 0x80808080u);
+    const uint32_t u = opaque(v);
 #pragma unroll
-    for (int k = k0; k < k1; ++k) t = fmaf((float)((u >> (8 * k)) & 0xFFu), xv[jb + k - k0], t);
+    for (int k = k0; k < k1; ++k) t = fmaf(sbyte(u, k), xv[jb + k - k0], t);
     return t;
 }
 
-// Stage x into LDS (padded layout) and the per-block bias terms.
-// For Q4 the upper half of each block is pre-scaled by 1/16 and bias[b] is
-// 8 * sum x_b; for Q8 x is stored as is and bias[b] is 128 * sum x_b.
-template <bool kQ4>
-__device__ __forceinline__ void stage_x(const float* __restrict__ x, float* xs, float* bias, int K) {
-    for (int i = threadIdx.x; i < K; i += kThreads) {
-        float v = x[i];
-        if (kQ4 && (i & 16)) v *= 0.0625f;
-        xs[xpad(i)] = v;
-    }
-    __syncthreads();
-    const int nb = K >> 5;
-    for (int b = threadIdx.x; b < nb; b += kThreads) {
-        const float* xb = xs + xpad(b * 32);  // a block never straddles a 64-float pad group
-        float s0 = 0.f, s1 = 0.f;
+// Stage x into LDS in the padded layout, transformed by the fused pre-op and
+// scaled by `scale` (1/16 for Q4, exact).
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, float* xs, int K, float scale, int pre,
+                                        const float* __restrict__ arg, float eps) {
+    if (pre == kPreRmsNorm) {
+        __shared__ float red[kWavesPerBlock];
+        float s = 0.f;
+        for (int i = threadIdx.x; i < K; i += kThreads) s = fmaf(x[i], x[i], s);
+        s = wave_sum(s);
+        if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x >> 6] = s;
+        __syncthreads();
+        float tot = 0.f;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            s0 += xb[j];
-            s1 += xb[16 + j];
+        for (int w = 0; w < kWavesPerBlock; ++w) tot += red[w];
+        const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+        for (int i = threadIdx.x; i < K; i += kThreads)
+            xs[xpad(i)] = __fmul_rn(__fmul_rn(__fmul_rn(x[i], inv), arg[i]), scale);
+    } else if (pre == kPreSwiGlu) {
+        for (int i = threadIdx.x; i < K; i += kThreads) {
+            const float g = x[i];
+            xs[xpad(i)] = __fmul_rn(__fmul_rn(g / (1.0f + expf(-g)), arg[i]), scale);
         }
-        bias[b] = kQ4 ? 8.0f * (s0 + 16.0f * s1) : 128.0f * (s0 + s1);
+    } else {
+        for (int i = threadIdx.x; i < K; i += kThreads) xs[xpad(i)] = x[i] * scale;
     }
     __syncthreads();
 }
@@ -99,11 +109,11 @@ template <int R, bool kGguf>
 __global__ __launch_bounds__(kThreads) void q4_matvec_pairs(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ wscale,
                                                             const float* __restrict__ x,
-                                                            float* __restrict__ y, int M, int K) {
-    extern __shared__ float smem[];
-    float* xs = smem;
-    float* bias = smem + K + (K >> 4);
-    stage_x<true>(x, xs, bias, K);
+                                                            float* __restrict__ y, int M, int K, int pre,
+                                                            const float* __restrict__ pre_arg, float eps,
+                                                            int accumulate) {
+    extern __shared__ float xs[];
+    stage_x(x, xs, K, 0.0625f, pre, pre_arg, eps);
 
     const int nb = K >> 5;
     const int np = nb >> 1;
@@ -155,7 +165,6 @@ __global__ __launch_bounds__(kThreads) void q4_matvec_pairs(const uint8_t* __res
                 const float4 t = xq[q];
                 xr[4 * q] = t.x; xr[4 * q + 1] = t.y; xr[4 * q + 2] = t.z; xr[4 * q + 3] = t.w;
             }
-            const float bA = bias[2 * pc], bB = bias[2 * pc + 1];
 
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -182,8 +191,8 @@ __global__ __launch_bounds__(kThreads) void q4_matvec_pairs(const uint8_t* __res
                     tB = q4_bytes<0, 4, 8>(v[r][6], xr + 32, xr + 48, tB);
                     tB = q4_bytes<0, 4, 12>(v[r][7], xr + 32, xr + 48, tB);
                 }
-                float a = fmaf(dA[r], tA - bA, acc[r]);
-                a = fmaf(dB[r], tB - bB, a);
+                float a = fmaf(dA[r], tA, acc[r]);
+                a = fmaf(dB[r], tB, a);
                 acc[r] = active ? a : acc[r];
             }
         }
@@ -191,7 +200,7 @@ __global__ __launch_bounds__(kThreads) void q4_matvec_pairs(const uint8_t* __res
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const float s = wave_sum(acc[r]);
-            if (lane == r && row0 + r < M) y[row0 + r] = s;
+            if (lane == r && row0 + r < M) y[row0 + r] = accumulate ? y[row0 + r] + s : s;
         }
     }
 }
@@ -203,11 +212,11 @@ template <int R, bool kGguf>
 __global__ __launch_bounds__(kThreads) void q8_matvec_pairs(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ wscale,
                                                             const float* __restrict__ x,
-                                                            float* __restrict__ y, int M, int K) {
-    extern __shared__ float smem[];
-    float* xs = smem;
-    float* bias = smem + K + (K >> 4);
-    stage_x<false>(x, xs, bias, K);
+                                                            float* __restrict__ y, int M, int K, int pre,
+                                                            const float* __restrict__ pre_arg, float eps,
+                                                            int accumulate) {
+    extern __shared__ float xs[];
+    stage_x(x, xs, K, 1.0f, pre, pre_arg, eps);
 
     const int nb = K >> 5;
     const int np = nb >> 1;
@@ -261,7 +270,6 @@ __global__ __launch_bounds__(kThreads) void q8_matvec_pairs(const uint8_t* __res
                 const float4 t = xq[q];
                 xr[4 * q] = t.x; xr[4 * q + 1] = t.y; xr[4 * q + 2] = t.z; xr[4 * q + 3] = t.w;
             }
-            const float bA = bias[2 * pc], bB = bias[2 * pc + 1];
 
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -282,8 +290,8 @@ __global__ __launch_bounds__(kThreads) void q8_matvec_pairs(const uint8_t* __res
 #pragma unroll
                     for (int q = 0; q < 8; ++q) tB = q8_bytes<0, 4, 0>(v[r][8 + q], xr + 32 + 4 * q, tB);
                 }
-                float a = fmaf(dA[r], tA - bA, acc[r]);
-                a = fmaf(dB[r], tB - bB, a);
+                float a = fmaf(dA[r], tA, acc[r]);
+                a = fmaf(dB[r], tB, a);
                 acc[r] = active ? a : acc[r];
             }
         }
@@ -291,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void q8_matvec_pairs(const uint8_t* __res
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const float s = wave_sum(acc[r]);
-            if (lane == r && row0 + r < M) y[row0 + r] = s;
+            if (lane == r && row0 + r < M) y[row0 + r] = accumulate ? y[row0 + r] + s : s;
         }
     }
 }
@@ -305,7 +313,7 @@ template <bool kQ8, bool kGguf>
 __global__ __launch_bounds__(kThreads) void matvec_generic(const uint8_t* __restrict__ w,
                                                            const float* __restrict__ wscale,
                                                            const float* __restrict__ x,
-                                                           float* __restrict__ y, int M, int K) {
+                                                           float* __restrict__ y, int M, int K, int accumulate) {
     const int nb = K >> 5;
     const int qbytes = kQ8 ? 32 : 16;
     const int64_t blk_bytes = kGguf ? qbytes + 2 : qbytes;
@@ -336,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void matvec_generic(const uint8_t* __rest
         acc = fmaf(d, t, acc);
     }
     acc = wave_sum(acc);
-    if (lane == 0) y[row] = acc;
+    if (lane == 0) y[row] = accumulate ? y[row] + acc : acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -360,7 +368,7 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t* __rest
     }
 }
 
-size_t pair_lds_bytes(int64_t K) { return (size_t)(K + K / 16 + K / 32) * sizeof(float); }
+size_t pair_lds_bytes(int64_t K) { return (size_t)(K + K / 16) * sizeof(float); }
 
 int pick_rows_per_wave(int64_t M, int r_max) {
     // Aim for at least ~8 waves per CU across 256 CUs before growing R.
@@ -370,31 +378,50 @@ int pick_rows_per_wave(int64_t M, int r_max) {
 }
 
 template <int R, bool kGguf>
-void launch_q4(const uint8_t* w, const float* s, const float* x, float* y, int M, int K, size_t lds,
-               hipStream_t st) {
+int launch_q4(const uint8_t* w, const float* s, const float* x, float* y, int M, int K, size_t lds,
+               hipStream_t st, const MatvecOpts& o) {
+    const int rc = dynamic_lds((const void*)q4_matvec_pairs<R, kGguf>, lds);
+    if (rc) return rc;
     const int64_t groups = (M + R - 1) / R;
     const int blocks = (int)((groups + kWavesPerBlock - 1) / kWavesPerBlock);
-    hipLaunchKernelGGL((q4_matvec_pairs<R, kGguf>), dim3(blocks), dim3(kThreads), lds, st, w, s, x, y, M, K);
+    hipLaunchKernelGGL((q4_matvec_pairs<R, kGguf>), dim3(blocks), dim3(kThreads), lds, st, w, s, x, y, M, K, o.pre,
+                       o.pre_arg, o.eps, (int)o.accumulate);
+    return kOk;
 }
 
 template <int R, bool kGguf>
-void launch_q8(const uint8_t* w, const float* s, const float* x, float* y, int M, int K, size_t lds,
-               hipStream_t st) {
+int launch_q8(const uint8_t* w, const float* s, const float* x, float* y, int M, int K, size_t lds,
+               hipStream_t st, const MatvecOpts& o) {
+    const int rc = dynamic_lds((const void*)q8_matvec_pairs<R, kGguf>, lds);
+    if (rc) return rc;
     const int64_t groups = (M + R - 1) / R;
     const int blocks = (int)((groups + kWavesPerBlock - 1) / kWavesPerBlock);
-    hipLaunchKernelGGL((q8_matvec_pairs<R, kGguf>), dim3(blocks), dim3(kThreads), lds, st, w, s, x, y, M, K);
+    hipLaunchKernelGGL((q8_matvec_pairs<R, kGguf>), dim3(blocks), dim3(kThreads), lds, st, w, s, x, y, M, K, o.pre,
+                       o.pre_arg, o.eps, (int)o.accumulate);
+    return kOk;
 }
 
-bool lds_opt_in_done = false;
+std::atomic<int> g_q4_kernel{kQ4KernelAuto};
 
 }  // namespace
 
+int set_q4_kernel(int kernel) {
+    if (kernel < kQ4KernelAuto || kernel > kQ4KernelMfma)
+        return fail(kInvalidArgument, "unknown Q4_0 matvec kernel selector %d", kernel);
+    g_q4_kernel.store(kernel);
+    return kOk;
+}
+
+int get_q4_kernel() { return g_q4_kernel.load(); }
+
 int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, const float* x, float* y,
-                  int64_t M, int64_t K, hipStream_t stream) {
+                  int64_t M, int64_t K, hipStream_t stream, const MatvecOpts& opts) {
     if (M <= 0 || K <= 0 || (K % 32) != 0)
         return fail(kInvalidArgument, "matvec: need M > 0, K > 0 and K %% 32 == 0 (got M=%lld K=%lld)",
                     (long long)M, (long long)K);
     if (M > INT32_MAX || K > INT32_MAX) return fail(kInvalidArgument, "matvec: M and K must fit in int32");
+    if (opts.pre != kPreNone && !opts.pre_arg) return fail(kInvalidArgument, "matvec: pre-op without its argument");
+    if (opts.pre < kPreNone || opts.pre > kPreSwiGlu) return fail(kInvalidArgument, "matvec: unknown pre-op %d", opts.pre);
     const int64_t nb = K / 32;
     const int64_t blk_bytes = qt == QuantType::Q4_0 ? (gguf ? 18 : 16) : (gguf ? 34 : 32);
     const int64_t total = M * nb * blk_bytes;
@@ -402,75 +429,70 @@ int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, c
     const size_t lds = pair_lds_bytes(K);
     const bool aligned = ((uintptr_t)w % 4 == 0) && (!gguf || nb % 2 == 0) && ((uintptr_t)scales % 8 == 0) &&
                          ((uintptr_t)x % 4 == 0);
-    const bool pairs = nb % 2 == 0 && aligned && lds <= 160 * 1024 && total < (int64_t)UINT32_MAX;
+    const bool pairs = nb % 2 == 0 && aligned && lds <= 160 * 1024 - 256 && total < (int64_t)UINT32_MAX;
     const int m = (int)M, k = (int)K;
 
-    if (!lds_opt_in_done) {
-        // Dynamic LDS beyond 64 KB needs an explicit opt-in per kernel.
-        const int max_lds = 160 * 1024;
-        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<1, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<2, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<4, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<8, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<1, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<2, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<4, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q4_matvec_pairs<8, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<1, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<2, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<4, true>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<1, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<2, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        (void)hipFuncSetAttribute((const void*)q8_matvec_pairs<4, false>, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds);
-        lds_opt_in_done = true;
-    }
+    int rc = kOk;
 
+    if (qt == QuantType::Q4_0 && gguf) {
+        const int sel = g_q4_kernel.load(std::memory_order_relaxed);
+        const bool mfma_ok = q4_0_mfma_eligible(w, x, opts, M, K);
+        if (sel == kQ4KernelMfma && !mfma_ok)
+            return fail(kUnsupported, "matvec: the MFMA Q4_0 kernel needs K %% 256 == 0, K <= 16384, "
+                                      "4-byte aligned blocks and 16-byte aligned x (got M=%lld K=%lld)",
+                        (long long)M, (long long)K);
+        if (sel != kQ4KernelFp32 && mfma_ok) return q4_0_mfma_launch(w, x, y, M, K, stream, opts);
+    }
     if (pairs && qt == QuantType::Q4_0) {
         const int r = pick_rows_per_wave(M, 8);
         if (gguf) {
             switch (r) {
-                case 8: launch_q4<8, true>(wb, scales, x, y, m, k, lds, stream); break;
-                case 4: launch_q4<4, true>(wb, scales, x, y, m, k, lds, stream); break;
-                case 2: launch_q4<2, true>(wb, scales, x, y, m, k, lds, stream); break;
-                default: launch_q4<1, true>(wb, scales, x, y, m, k, lds, stream); break;
+                case 8: rc = launch_q4<8, true>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                case 4: rc = launch_q4<4, true>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                case 2: rc = launch_q4<2, true>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                default: rc = launch_q4<1, true>(wb, scales, x, y, m, k, lds, stream, opts); break;
             }
         } else {
             switch (r) {
-                case 8: launch_q4<8, false>(wb, scales, x, y, m, k, lds, stream); break;
-                case 4: launch_q4<4, false>(wb, scales, x, y, m, k, lds, stream); break;
-                case 2: launch_q4<2, false>(wb, scales, x, y, m, k, lds, stream); break;
-                default: launch_q4<1, false>(wb, scales, x, y, m, k, lds, stream); break;
+                case 8: rc = launch_q4<8, false>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                case 4: rc = launch_q4<4, false>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                case 2: rc = launch_q4<2, false>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                default: rc = launch_q4<1, false>(wb, scales, x, y, m, k, lds, stream, opts); break;
             }
         }
     } else if (pairs) {
         const int r = pick_rows_per_wave(M, 4);
         if (gguf) {
             switch (r) {
-                case 4: launch_q8<4, true>(wb, scales, x, y, m, k, lds, stream); break;
-                case 2: launch_q8<2, true>(wb, scales, x, y, m, k, lds, stream); break;
-                default: launch_q8<1, true>(wb, scales, x, y, m, k, lds, stream); break;
+                case 4: rc = launch_q8<4, true>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                case 2: rc = launch_q8<2, true>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                default: rc = launch_q8<1, true>(wb, scales, x, y, m, k, lds, stream, opts); break;
             }
         } else {
             switch (r) {
-                case 4: launch_q8<4, false>(wb, scales, x, y, m, k, lds, stream); break;
-                case 2: launch_q8<2, false>(wb, scales, x, y, m, k, lds, stream); break;
-                default: launch_q8<1, false>(wb, scales, x, y, m, k, lds, stream); break;
+                case 4: rc = launch_q8<4, false>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                case 2: rc = launch_q8<2, false>(wb, scales, x, y, m, k, lds, stream, opts); break;
+                default: rc = launch_q8<1, false>(wb, scales, x, y, m, k, lds, stream, opts); break;
             }
         }
     } else {
+        if (opts.pre != kPreNone)
+            return fail(kUnsupported, "matvec: fused pre-ops need K %% 64 == 0, dword-aligned rows and K <= 37000");
         const int blocks = (int)((M + kWavesPerBlock - 1) / kWavesPerBlock);
+        const int acc = (int)opts.accumulate;
         if (qt == QuantType::Q4_0) {
             if (gguf)
-                hipLaunchKernelGGL((matvec_generic<false, true>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k);
+                hipLaunchKernelGGL((matvec_generic<false, true>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k, acc);
             else
-                hipLaunchKernelGGL((matvec_generic<false, false>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k);
+                hipLaunchKernelGGL((matvec_generic<false, false>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k, acc);
         } else {
             if (gguf)
-                hipLaunchKernelGGL((matvec_generic<true, true>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k);
+                hipLaunchKernelGGL((matvec_generic<true, true>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k, acc);
             else
-                hipLaunchKernelGGL((matvec_generic<true, false>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k);
+                hipLaunchKernelGGL((matvec_generic<true, false>), dim3(blocks), dim3(kThreads), 0, stream, wb, scales, x, y, m, k, acc);
         }
     }
+    if (rc) return rc;
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

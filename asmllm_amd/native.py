@@ -9,7 +9,7 @@ argtypes its callers set (test_runner.py:94-101, 199-207, 384-390, 408-414,
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p, c_char_p, POINTER
+from ctypes import c_float, c_int, c_int64, c_size_t, c_uint64, c_void_p, c_char_p, POINTER
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -17,6 +17,13 @@ LIB_PATH = PKG / "lib" / "libasmllm.so"
 HEADER_PATH = PKG.parent / "include" / "asmllm_hip.h"
 
 _P = c_void_p
+
+# Values of the header's #defines.
+Q4_0 = 2
+Q8_0 = 8
+PRE_NONE, PRE_RMSNORM, PRE_SWIGLU = 0, 1, 2
+Q4_KERNEL_AUTO, Q4_KERNEL_FP32, Q4_KERNEL_MFMA = 0, 1, 2
+OK, ERR_INVALID_ARGUMENT, ERR_HIP, ERR_UNSUPPORTED, ERR_NO_DEVICE = 0, -1, -2, -3, -4
 # name -> (restype, argtypes)
 SIGNATURES: dict[str, tuple] = {
     # reference-named entry points
@@ -29,6 +36,11 @@ SIGNATURES: dict[str, tuple] = {
     "asm_threadpool_init": (None, [c_int]),
     "asm_threadpool_shutdown": (None, []),
     "asm_threadpool_get_num_threads": (c_int, []),
+    "asm_rmsnorm": (None, [_P, _P, _P, c_int64, c_float]),
+    "asm_rope": (None, [_P, _P, c_int64, c_int64, c_float]),
+    "asm_softmax": (None, [_P, _P, c_int64]),
+    "asm_silu_hadamard": (None, [_P, _P, c_int64]),
+    "asm_attention": (None, [_P, _P, _P, _P, c_int64, c_int64, c_float]),
     # device entry points
     "asmhip_matmul_q4_0": (c_int, [_P, _P, _P, c_int64, c_int64, _P]),
     "asmhip_matmul_q8_0": (c_int, [_P, _P, _P, c_int64, c_int64, _P]),
@@ -36,6 +48,23 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_matmul_q8_split": (c_int, [_P, _P, _P, _P, c_int64, c_int64, _P]),
     "asmhip_dequantize_q4_0": (c_int, [_P, _P, c_int64, c_int64, _P]),
     "asmhip_dequantize_q8_0": (c_int, [_P, _P, c_int64, c_int64, _P]),
+    "asmhip_matmul_fused": (c_int, [c_int, _P, _P, _P, c_int64, c_int64, c_int, _P, c_float, c_int, _P]),
+    "asmhip_set_q4_kernel": (c_int, [c_int]),
+    "asmhip_get_q4_kernel": (c_int, []),
+    "asmhip_quantize": (c_int, [c_int, _P, _P, c_int64, c_int64, _P]),
+    "asmhip_random_blocks": (c_int, [c_int, _P, c_int64, c_int64, c_uint64, c_float, _P]),
+    "asmhip_random_f16": (c_int, [_P, c_int64, c_uint64, c_float, _P]),
+    "asmhip_fill_f32": (c_int, [_P, c_int64, c_float, _P]),
+    "asmhip_rmsnorm": (c_int, [_P, _P, _P, c_int64, c_float, _P]),
+    "asmhip_rope": (c_int, [_P, _P, c_int64, c_int64, c_int64, _P, c_int64, c_float, _P]),
+    "asmhip_softmax": (c_int, [_P, _P, c_int64, _P]),
+    "asmhip_silu_hadamard": (c_int, [_P, _P, c_int64, _P]),
+    "asmhip_attention": (c_int, [_P, _P, _P, _P, c_int64, c_int64, c_float, _P]),
+    "asmhip_rope_kv_write": (c_int, [_P, _P, _P, c_int, c_int, c_int, _P, c_int, c_float, _P]),
+    "asmhip_attention_decode_workspace": (c_int64, [c_int, c_int, c_int]),
+    "asmhip_attention_decode": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, _P]),
+    "asmhip_embed_q4_0": (c_int, [_P, _P, _P, c_int, c_int, _P]),
+    "asmhip_argmax": (c_int, [_P, c_int, _P, _P, _P]),
     # plumbing
     "asmhip_device_count": (c_int, []),
     "asmhip_device_info": (c_int, [c_char_p, c_size_t, POINTER(c_int), POINTER(c_int), POINTER(c_size_t)]),

@@ -43,6 +43,20 @@ extern "C" {
 #define ASMHIP_ERR_UNSUPPORTED (-3)
 #define ASMHIP_ERR_NO_DEVICE (-4)
 
+/* Block types, numbered as GGUF tensor types (src/runtime/generate.py:175-178). */
+#define ASMHIP_Q4_0 2
+#define ASMHIP_Q8_0 8
+
+/* Work fused into a matvec's read of x (asmhip_matmul_fused). */
+#define ASMHIP_PRE_NONE 0
+#define ASMHIP_PRE_RMSNORM 1 /* x <- (x * 1/sqrt(mean(x^2) + eps)) * pre_arg */
+#define ASMHIP_PRE_SWIGLU 2  /* x <- x / (1 + exp(-x)) * pre_arg             */
+
+/* Q4_0 GGUF kernel selection (asmhip_set_q4_kernel). */
+#define ASMHIP_Q4_KERNEL_AUTO 0 /* int8 MFMA kernel where eligible, else fp32 */
+#define ASMHIP_Q4_KERNEL_FP32 1 /* fp32 VALU kernel only                      */
+#define ASMHIP_Q4_KERNEL_MFMA 2 /* int8 MFMA kernel only (others: UNSUPPORTED) */
+
 /* ---- 1. reference-named entry points ------------------------------------ */
 
 /* src/kernels/x86_64/matmul_q4_avx2.asm:11-19, 57: y = W x, split layout. */
@@ -75,6 +89,22 @@ ASMHIP_API void asm_threadpool_shutdown(void);
 /* src/runtime/threadpool.h:102 / threadpool.c:386-388. */
 ASMHIP_API int asm_threadpool_get_num_threads(void);
 
+/* Decode-step ops (build_kernel.py:85-104 export list; argtypes
+ * test_runner.py:199-296; call sites generate.py:261-326). */
+/* y = (x * (1/sqrt(mean(x^2) + eps))) * w   (rmsnorm_avx2.asm:63-151) */
+ASMHIP_API void asm_rmsnorm(const float* x, const float* w, float* y, int64_t dim, float eps);
+/* In place on one head of q and one of k: pairs (2p, 2p+1) rotated by
+ * pos * theta^(-2p/head_dim)   (rope_avx2.asm:52-146) */
+ASMHIP_API void asm_rope(float* q, float* k, int64_t head_dim, int64_t pos, float theta);
+/* y = exp(x - max) / sum, x == y allowed   (softmax_avx2.asm:48-130) */
+ASMHIP_API void asm_softmax(const float* x, float* y, int64_t dim);
+/* gate = gate / (1 + exp(-gate)) * up   (swiglu_avx2.asm:45-81) */
+ASMHIP_API void asm_silu_hadamard(float* gate, const float* up, int64_t dim);
+/* y = softmax(q k^T * scale) v, q/k/v/y [seq_len][head_dim]
+ * (attention_avx2.asm:59-218) */
+ASMHIP_API void asm_attention(const float* q, const float* k, const float* v, float* y, int64_t seq_len,
+                              int64_t head_dim, float scale);
+
 /* ---- 2. device entry points (hot path) ----------------------------------- */
 
 /* Q4_0 matvec over GGUF blocks resident in HBM: y[M] = W[M][K] x[K].  Block
@@ -95,6 +125,63 @@ ASMHIP_API int asmhip_matmul_q8_split(const int8_t* qweights, const float* scale
  * (tests/reference/ops.py:16-30, 44-53). */
 ASMHIP_API int asmhip_dequantize_q4_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream);
 ASMHIP_API int asmhip_dequantize_q8_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream);
+
+/* GGUF-block matvec with work fused around it, as forward_token sequences it
+ * (generate.py:261-326): pre_op transforms x while it is read (RMSNorm with
+ * weights pre_arg, or SwiGLU with x = gate and pre_arg = up), and accumulate
+ * != 0 adds W x into y (the residual add) instead of overwriting y. */
+ASMHIP_API int asmhip_matmul_fused(int qtype, const void* blocks, const float* x, float* y, int64_t M, int64_t K,
+                                   int pre_op, const float* pre_arg, float eps, int accumulate, void* stream);
+/* Process-wide Q4_0 GGUF kernel choice (ASMHIP_Q4_KERNEL_*). */
+ASMHIP_API int asmhip_set_q4_kernel(int kernel);
+ASMHIP_API int asmhip_get_q4_kernel(void);
+
+/* fp32 rows -> GGUF blocks on the GPU: Q4_0 d = m / -8 (m the first element of
+ * largest magnitude), q = min(15, trunc(w / d + 8.5)); Q8_0 d = amax / 127,
+ * q = round-half-even(w * 127 / amax) saturated (matmul_q4_neon.S:80-135);
+ * d stored as fp16 (round to nearest even). */
+ASMHIP_API int asmhip_quantize(int qtype, const float* w, void* blocks, int64_t rows, int64_t K, void* stream);
+/* Synthetic model data generated in HBM: blocks of N(0, stddev^2) weights
+ * quantized as above, fp16 N(0, stddev^2) values, or a constant fill. */
+ASMHIP_API int asmhip_random_blocks(int qtype, void* blocks, int64_t rows, int64_t K, uint64_t seed, float stddev,
+                                    void* stream);
+ASMHIP_API int asmhip_random_f16(void* out, int64_t n, uint64_t seed, float stddev, void* stream);
+ASMHIP_API int asmhip_fill_f32(float* out, int64_t n, float value, void* stream);
+
+/* Device-pointer forms of the decode-step ops.  asmhip_rope rotates
+ * n_q_heads heads of q and n_k_heads heads of k; the position is *pos_dev
+ * when pos_dev is not NULL (read on the GPU, so a captured graph follows it),
+ * else pos. */
+ASMHIP_API int asmhip_rmsnorm(const float* x, const float* w, float* y, int64_t dim, float eps, void* stream);
+ASMHIP_API int asmhip_rope(float* q, float* k, int64_t n_q_heads, int64_t n_k_heads, int64_t head_dim,
+                           const int* pos_dev, int64_t pos, float theta, void* stream);
+ASMHIP_API int asmhip_softmax(const float* x, float* y, int64_t dim, void* stream);
+ASMHIP_API int asmhip_silu_hadamard(float* gate, const float* up, int64_t dim, void* stream);
+ASMHIP_API int asmhip_attention(const float* q, const float* k, const float* v, float* y, int64_t seq_len,
+                                int64_t head_dim, float scale, void* stream);
+
+/* Decode attention over an fp16 KV cache (generate.py:283-296 with the cache
+ * kept on the GPU in fp16).  qkv = [q (n_heads*head_dim) | k | v
+ * (n_kv_heads*head_dim each)]; caches are head-major
+ * [n_kv_heads][max_ctx][head_dim] fp16.  asmhip_rope_kv_write rotates q in
+ * place and writes rotated k and v at position *pos_dev.
+ * asmhip_attention_decode computes, per head h (kv head h / (n_heads /
+ * n_kv_heads)), softmax(q_h . k_p / sqrt(head_dim)) . v_p over positions
+ * 0..*pos_dev; workspace holds asmhip_attention_decode_workspace() floats.
+ * head_dim 64 or 128. */
+ASMHIP_API int asmhip_rope_kv_write(float* qkv, void* k_cache, void* v_cache, int n_heads, int n_kv_heads,
+                                    int head_dim, const int* pos_dev, int max_ctx, float theta, void* stream);
+ASMHIP_API int64_t asmhip_attention_decode_workspace(int n_heads, int head_dim, int max_ctx);
+ASMHIP_API int asmhip_attention_decode(const float* q, const void* k_cache, const void* v_cache, float* workspace,
+                                       float* out, int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
+                                       int max_ctx, void* stream);
+/* x = row *token_dev of a Q4_0 embedding table [n_vocab][dim]
+ * (generate.py:262, the table dequantized by get_tensor :169-182). */
+ASMHIP_API int asmhip_embed_q4_0(const void* table, const int* token_dev, float* x, int n_vocab, int dim,
+                                 void* stream);
+/* *token_dev = first index of max(logits) (numpy.argmax, generate.py:419-420);
+ * then ++*pos_dev when pos_dev is not NULL. */
+ASMHIP_API int asmhip_argmax(const float* logits, int n, int* token_dev, int* pos_dev, void* stream);
 
 /* ---- device memory, streams, events (so a ctypes host needs no other GPU
  *      binding; the reference's buffers are numpy arrays) ----------------- */

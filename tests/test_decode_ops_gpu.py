@@ -1,0 +1,233 @@
+"""GPU parity of the decode-step ops, the GPU quantizers and the synthetic
+model generators (through the C ABI) against the CPU oracle.
+
+Bar: the reference's fp32 tolerance for these ops (1e-5, test_runner.py:36),
+fp16 cache entries within one fp16 rounding, quantized bytes bit-exact.
+"""
+
+import numpy as np
+import pytest
+
+from asmllm_amd import gguf, native
+from asmllm_amd.device import DeviceBuffer, synchronize
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _host(fn, *args):
+    fn(*[a.ctypes.data if isinstance(a, np.ndarray) else a for a in args])
+
+
+def _ok(hip, rc):
+    assert rc == 0, hip.asmhip_last_error()
+
+
+# ---- reference-named ops on host buffers ---------------------------------------------------
+
+@pytest.mark.parametrize("dim", [1, 33, 4096, 11008])
+def test_rmsnorm(hip, oracle, dim):
+    rng = np.random.default_rng(dim)
+    x = rng.standard_normal(dim).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, dim).astype(np.float32)
+    for eps in (1e-5, 1e-6):
+        y = np.zeros(dim, np.float32)
+        _host(hip.asm_rmsnorm, x, w, y, dim, eps)
+        np.testing.assert_allclose(y, oracle.rmsnorm(x, w, eps), rtol=TOL, atol=TOL)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("pos", [0, 1, 17, 2047, 2175, 100000])
+def test_rope(hip, oracle, hd, pos):
+    rng = np.random.default_rng(hd + pos)
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.standard_normal(hd).astype(np.float32)
+    q_ref, k_ref = oracle.rope(q, k, hd, pos, 10000.0)
+    _host(hip.asm_rope, q, k, hd, pos, 10000.0)
+    np.testing.assert_allclose(q, q_ref, rtol=TOL, atol=TOL)
+    np.testing.assert_allclose(k, k_ref, rtol=TOL, atol=TOL)
+
+
+def test_rope_position_zero_is_identity(hip):
+    q = np.arange(128, dtype=np.float32)
+    k = -np.arange(128, dtype=np.float32)
+    q0, k0 = q.copy(), k.copy()
+    _host(hip.asm_rope, q, k, 128, 0, 10000.0)
+    np.testing.assert_array_equal(q, q0)
+    np.testing.assert_array_equal(k, k0)
+
+
+@pytest.mark.parametrize("dim", [1, 7, 2049, 32000])
+def test_softmax(hip, oracle, dim):
+    rng = np.random.default_rng(dim)
+    x = (rng.standard_normal(dim) * 4).astype(np.float32)
+    y = np.zeros(dim, np.float32)
+    _host(hip.asm_softmax, x, y, dim)
+    e = np.exp(x.astype(np.float64) - x.max())
+    np.testing.assert_allclose(y, e / e.sum(), rtol=TOL, atol=1e-12)
+    # the reference sums exp() sequentially in fp32 (softmax_avx2.asm:65-97): its
+    # result carries up to (dim - 1) roundings of the sum on top of the bar
+    np.testing.assert_allclose(y, oracle.softmax(x), rtol=TOL + dim * 2.0 ** -24, atol=1e-12)
+    assert abs(float(y.astype(np.float64).sum()) - 1.0) < 1e-5
+    inplace = x.copy()
+    _host(hip.asm_softmax, inplace, inplace, dim)  # x == y (attention_avx2.asm:141-142)
+    np.testing.assert_array_equal(inplace, y)
+
+
+@pytest.mark.parametrize("dim", [1, 100, 11008])
+def test_silu_hadamard(hip, oracle, dim):
+    rng = np.random.default_rng(dim)
+    g = (rng.standard_normal(dim) * 3).astype(np.float32)
+    u = rng.standard_normal(dim).astype(np.float32)
+    ref = oracle.silu_hadamard(g, u)
+    _host(hip.asm_silu_hadamard, g, u, dim)
+    np.testing.assert_allclose(g, ref, rtol=TOL, atol=1e-7)
+
+
+@pytest.mark.parametrize("seq,hd", [(1, 64), (7, 64), (128, 128), (300, 128)])
+def test_attention(hip, oracle, seq, hd):
+    rng = np.random.default_rng(seq * hd)
+    q, k, v = (rng.standard_normal((seq, hd)).astype(np.float32) for _ in range(3))
+    scale = float(1.0 / np.sqrt(hd))
+    y = np.zeros((seq, hd), np.float32)
+    _host(hip.asm_attention, q, k, v, y, seq, hd, scale)
+    s64 = (q.astype(np.float64) @ k.astype(np.float64).T) * scale
+    p64 = np.exp(s64 - s64.max(axis=1, keepdims=True))
+    ref64 = (p64 / p64.sum(axis=1, keepdims=True)) @ v.astype(np.float64)
+    np.testing.assert_allclose(y, ref64, rtol=TOL, atol=TOL)
+    # the reference's sequential fp32 softmax sum adds up to seq roundings
+    np.testing.assert_allclose(y, oracle.attention(q, k, v, scale), rtol=TOL + seq * 2.0 ** -24, atol=TOL)
+
+
+# ---- device forms used by the decode step ----------------------------------------------------
+
+def test_multi_head_rope_reads_position_on_device(hip, oracle):
+    n_q, n_k, hd, pos = 32, 8, 128, 1234
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((n_q, hd)).astype(np.float32)
+    k = rng.standard_normal((n_k, hd)).astype(np.float32)
+    dq, dk = DeviceBuffer.from_numpy(q), DeviceBuffer.from_numpy(k)
+    dpos = DeviceBuffer.from_numpy(np.array([pos], np.int32))
+    _ok(hip, hip.asmhip_rope(dq.ptr, dk.ptr, n_q, n_k, hd, dpos.ptr, 0, 10000.0, None))
+    synchronize()
+    gq, gk = dq.download(np.float32, (n_q, hd)), dk.download(np.float32, (n_k, hd))
+    for h in range(n_q):
+        rq, rk = oracle.rope(q[h], k[h % n_k], hd, pos, 10000.0)
+        np.testing.assert_allclose(gq[h], rq, rtol=TOL, atol=TOL)
+        if h < n_k:
+            np.testing.assert_allclose(gk[h], rk, rtol=TOL, atol=TOL)
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd,pos,max_ctx", [
+    (32, 32, 128, 0, 256), (32, 32, 128, 2047, 2176), (32, 8, 128, 700, 1024), (8, 2, 64, 129, 130),
+])
+def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos, max_ctx):
+    rng = np.random.default_rng(n_heads * 1000 + pos)
+    qkv = rng.standard_normal((n_heads + 2 * n_kv) * hd).astype(np.float32)
+    # caches head-major [n_kv][max_ctx][hd]; positions < pos hold earlier tokens
+    kc = np.zeros((n_kv, max_ctx, hd), np.float16)
+    vc = np.zeros((n_kv, max_ctx, hd), np.float16)
+    kc[:, :pos] = rng.standard_normal((n_kv, pos, hd))
+    vc[:, :pos] = rng.standard_normal((n_kv, pos, hd))
+    dqkv, dkc, dvc = DeviceBuffer.from_numpy(qkv), DeviceBuffer.from_numpy(kc), DeviceBuffer.from_numpy(vc)
+    dpos = DeviceBuffer.from_numpy(np.array([pos], np.int32))
+    ws = hip.asmhip_attention_decode_workspace(n_heads, hd, max_ctx)
+    assert ws > 0
+    dws, dout = DeviceBuffer(ws * 4), DeviceBuffer(n_heads * hd * 4)
+    _ok(hip, hip.asmhip_rope_kv_write(dqkv.ptr, dkc.ptr, dvc.ptr, n_heads, n_kv, hd, dpos.ptr, max_ctx, 10000.0,
+                                      None))
+    _ok(hip, hip.asmhip_attention_decode(dqkv.ptr, dkc.ptr, dvc.ptr, dws.ptr, dout.ptr, n_heads, n_kv, hd,
+                                         dpos.ptr, max_ctx, None))
+    synchronize()
+
+    q = qkv[: n_heads * hd].reshape(n_heads, hd)
+    k = qkv[n_heads * hd: (n_heads + n_kv) * hd].reshape(n_kv, hd)
+    v = qkv[(n_heads + n_kv) * hd:].reshape(n_kv, hd)
+    q_rot = np.stack([oracle.rope(q[h], k[0], hd, pos, 10000.0)[0] for h in range(n_heads)])
+    k_rot = np.stack([oracle.rope(q[0], k[h], hd, pos, 10000.0)[1] for h in range(n_kv)])
+    got_q = dqkv.download(np.float32, n_heads * hd).reshape(n_heads, hd)
+    np.testing.assert_allclose(got_q, q_rot, rtol=TOL, atol=TOL)
+    got_kc = dkc.download(np.float16, (n_kv, max_ctx, hd))
+    got_vc = dvc.download(np.float16, (n_kv, max_ctx, hd))
+    np.testing.assert_array_equal(got_vc[:, pos], v.astype(np.float16))
+    np.testing.assert_allclose(got_kc[:, pos].astype(np.float32), k_rot, rtol=2 ** -10, atol=1e-6)
+    np.testing.assert_array_equal(got_kc[:, :pos], kc[:, :pos])  # earlier positions untouched
+    if pos + 1 < max_ctx:
+        assert not got_kc[:, pos + 1:].any()
+
+    # oracle cache layout [pos][kv_head][hd], fp16 bits; the GPU's own k entry
+    kc_o = np.ascontiguousarray(got_kc.transpose(1, 0, 2)).view(np.uint16)
+    vc_o = np.ascontiguousarray(got_vc.transpose(1, 0, 2)).view(np.uint16)
+    ref = oracle.attention_decode_f16(got_q, kc_o, vc_o, pos + 1, n_kv, 8)
+    np.testing.assert_allclose(dout.download(np.float32, (n_heads, hd)), ref, rtol=TOL, atol=TOL)
+
+
+def test_embed_row_and_argmax(hip, oracle):
+    n_vocab, dim = 1000, 256
+    rng = np.random.default_rng(4)
+    table = gguf.quantize_q4_0(rng.standard_normal((n_vocab, dim)).astype(np.float32))
+    dt = DeviceBuffer.from_numpy(table)
+    dtok = DeviceBuffer.from_numpy(np.array([417], np.int32))
+    dx = DeviceBuffer(dim * 4)
+    _ok(hip, hip.asmhip_embed_q4_0(dt.ptr, dtok.ptr, dx.ptr, n_vocab, dim, None))
+    synchronize()
+    np.testing.assert_array_equal(dx.download(np.float32, dim), oracle.dequantize_q4_0(table[417:418])[0])
+
+    logits = rng.standard_normal(32000).astype(np.float32)
+    logits[[123, 31000]] = 9.0  # tie: the first index wins, as numpy.argmax
+    dl = DeviceBuffer.from_numpy(logits)
+    dpos = DeviceBuffer.from_numpy(np.array([41], np.int32))
+    _ok(hip, hip.asmhip_argmax(dl.ptr, 32000, dtok.ptr, dpos.ptr, None))
+    synchronize()
+    assert int(dtok.download(np.int32, 1)[0]) == int(np.argmax(logits)) == 123
+    assert int(dpos.download(np.int32, 1)[0]) == 42
+
+
+# ---- GPU quantizers and synthetic weights -----------------------------------------------------
+
+@pytest.mark.parametrize("qt", ["q4", "q8"])
+def test_gpu_quantizer_bit_exact(hip, oracle, qt):
+    rng = np.random.default_rng(12)
+    rows, K = 513, 4096
+    w = (rng.standard_normal((rows, K)) * 0.02).astype(np.float32)
+    w[0, :32] = 0.0                       # all-zero block
+    w[1, :32] = np.float32(0.5)           # constant block
+    w[2, :32] = np.linspace(-1, 1, 32)    # exact ties
+    m = float(np.abs(w[3, :32]).max())
+    w[3, 5], w[3, 9] = -m, m              # repeated magnitude: the first one sets the sign of d
+    dw, db = DeviceBuffer.from_numpy(w), DeviceBuffer(rows * (K // 32) * (18 if qt == "q4" else 34))
+    code = native.Q4_0 if qt == "q4" else native.Q8_0
+    _ok(hip, hip.asmhip_quantize(code, dw.ptr, db.ptr, rows, K, None))
+    synchronize()
+    bpb = 18 if qt == "q4" else 34
+    got = db.download(np.uint8, (rows, K // 32, bpb))
+    ref = oracle.quantize_q4_0(w) if qt == "q4" else oracle.quantize_q8_0(w)
+    bad = np.argwhere(got != ref)
+    assert bad.size == 0, f"mismatched bytes at {bad[:8].tolist()}: got {got[tuple(bad[:8].T)]}, want {ref[tuple(bad[:8].T)]}"
+    np.testing.assert_array_equal(ref, gguf.quantize_q4_0(w) if qt == "q4" else gguf.quantize_q8_0(w))
+
+
+@pytest.mark.parametrize("qt", ["q4", "q8"])
+def test_random_blocks_are_deterministic_and_distributed(hip, oracle, qt):
+    rows, K, std = 256, 4096, 0.02
+    code, bpb = (native.Q4_0, 18) if qt == "q4" else (native.Q8_0, 34)
+    a, b, c = (DeviceBuffer(rows * (K // 32) * bpb) for _ in range(3))
+    _ok(hip, hip.asmhip_random_blocks(code, a.ptr, rows, K, 7, std, None))
+    _ok(hip, hip.asmhip_random_blocks(code, b.ptr, rows, K, 7, std, None))
+    _ok(hip, hip.asmhip_random_blocks(code, c.ptr, rows, K, 8, std, None))
+    synchronize()
+    ba, bb, bc = (d.download(np.uint8, (rows, K // 32, bpb)) for d in (a, b, c))
+    np.testing.assert_array_equal(ba, bb)
+    assert (ba != bc).mean() > 0.5
+    w = oracle.dequantize_q4_0(ba) if qt == "q4" else oracle.dequantize_q8_0(ba)
+    assert abs(float(w.mean())) < 1e-3
+    assert 0.8 * std < float(w.std()) < 1.2 * std
+
+    h = DeviceBuffer(100001 * 2)
+    _ok(hip, hip.asmhip_random_f16(h.ptr, 100001, 3, 1.0, None))
+    f = DeviceBuffer(1000 * 4)
+    _ok(hip, hip.asmhip_fill_f32(f.ptr, 1000, 1.5, None))
+    synchronize()
+    v = h.download(np.float16, 100001).astype(np.float64)
+    assert abs(v.mean()) < 0.02 and 0.97 < v.std() < 1.03
+    assert np.all(f.download(np.float32, 1000) == 1.5)

@@ -11,7 +11,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from asmllm_amd import gguf
+from asmllm_amd import gguf, native
 from asmllm_amd.device import DeviceBuffer, synchronize
 from conftest import assert_matvec_close
 from oracle import golden as golden_mod
@@ -37,6 +37,19 @@ def _gguf_matvec(hip, qt, blocks, x):
     assert rc == 0, hip.asmhip_last_error()
     synchronize()
     return dy.download(np.float32, M)
+
+
+@pytest.fixture
+def q4_kernel(hip):
+    """Selects the Q4_0 GGUF kernel for one test; auto selection is restored after."""
+    def select(kernel):
+        assert hip.asmhip_set_q4_kernel(kernel) == 0, hip.asmhip_last_error()
+        assert hip.asmhip_get_q4_kernel() == kernel
+    yield select
+    hip.asmhip_set_q4_kernel(native.Q4_KERNEL_AUTO)
+
+
+Q4_KERNELS = [native.Q4_KERNEL_FP32, native.Q4_KERNEL_MFMA]
 
 
 def _host_call(fn, *arrays_and_ints):
@@ -164,10 +177,30 @@ def test_ragged_shapes(hip, oracle, qt, M, K):
 
 def test_all_eight_nibbles_give_zero(hip):
     blocks = np.zeros((64, 128, 18), np.uint8)
-    blocks[..., 0:2] = np.float16(0.37).view(np.uint8)
+    blocks[..., 0:2] = np.array([0.37], np.float16).view(np.uint8)
     blocks[..., 2:] = 0x88
     x = np.random.default_rng(1).standard_normal(4096).astype(np.float32)
     assert np.all(_gguf_matvec(hip, "q4", blocks, x) == 0.0)
+
+
+def test_near_constant_rows_keep_relative_accuracy(hip, oracle):
+    """Rows whose nibbles are all 8 but one, against an x with one small entry
+    where the weight is nonzero and large entries elsewhere: the row's L1 is
+    tiny, so any cancellation between large terms would break the bar."""
+    M, K = 64, 4096
+    blocks = np.zeros((M, K // 32, 18), np.uint8)
+    blocks[..., 0:2] = np.array([0.01], np.float16).view(np.uint8)
+    blocks[..., 2:] = 0x88
+    rng = np.random.default_rng(77)
+    cols = rng.integers(0, K, M)
+    for m, c in enumerate(cols):
+        b, j = divmod(int(c), 32)
+        byte = 2 + (j % 16)
+        blocks[m, b, byte] = (blocks[m, b, byte] & (0x0F if j >= 16 else 0xF0)) | ((9 << 4) if j >= 16 else 9)
+    x = (rng.standard_normal(K) * 1e4).astype(np.float32)
+    x[cols] = 1e-3
+    y = _gguf_matvec(hip, "q4", blocks, x)
+    assert_matvec_close(y, oracle.matmul_q4_0_gguf(blocks, x), oracle.dequantize_q4_0(blocks), x)
 
 
 def test_zero_scale_gives_zero(hip):
@@ -216,7 +249,114 @@ def test_split_layout_device_pointers(hip, oracle):
 
 def test_bad_arguments_are_rejected(hip):
     dx, dy, db = DeviceBuffer(4096 * 4), DeviceBuffer(64 * 4), DeviceBuffer(64 * 128 * 18)
-    assert hip.asmhip_matmul_q4_0(db.ptr, dx.ptr, dy.ptr, 64, 4000, None) == -1
+    assert hip.asmhip_matmul_q4_0(db.ptr, dx.ptr, dy.ptr, 64, 4010, None) == -1
     assert "K % 32" in hip.asmhip_last_error().decode()
     assert hip.asmhip_matmul_q4_0(db.ptr, dx.ptr, dy.ptr, 0, 4096, None) == -1
     assert hip.asmhip_matmul_q4_0(None, dx.ptr, dy.ptr, 64, 4096, None) == -1
+
+
+# ---- both Q4_0 GGUF kernels, selected explicitly ------------------------------------------
+
+@pytest.mark.parametrize("kernel", Q4_KERNELS, ids=["fp32", "mfma"])
+@pytest.mark.parametrize("M,K", [s[1:] for s in CONFIG_SHAPES if s[0] == "q4"] + [(16, 256), (40, 16384)])
+def test_q4_kernels_at_config_shapes(hip, oracle, q4_kernel, kernel, M, K):
+    q4_kernel(kernel)
+    blocks, x = _weights(3 * M + K, M, K)
+    y = _gguf_matvec(hip, "q4", blocks, x)
+    worst = assert_matvec_close(y, oracle.matmul_q4_0_gguf(blocks, x, NT), oracle.dequantize_q4_0(blocks), x)
+    print(f"kernel {kernel} {M}x{K}: max err / row L1 = {worst:.2e}")
+
+
+@pytest.mark.parametrize("kernel", Q4_KERNELS, ids=["fp32", "mfma"])
+def test_q4_kernels_edge_cases(hip, oracle, q4_kernel, kernel):
+    q4_kernel(kernel)
+    test_all_eight_nibbles_give_zero(hip)
+    test_near_constant_rows_keep_relative_accuracy(hip, oracle)
+    test_zero_scale_gives_zero(hip)
+    for col in (0, 15, 16, 31, 4064, 4095):
+        test_one_hot_x_picks_column_exactly(hip, oracle, "q4", col)
+
+
+def test_mfma_kernel_wide_dynamic_range_of_x(hip, oracle, q4_kernel):
+    """x spanning up to 2^40 inside a block, with zero weights placed on the
+    largest entries of some rows: the two-level fixed point keeps every row
+    within the bar."""
+    q4_kernel(native.Q4_KERNEL_MFMA)
+    rng = np.random.default_rng(90)
+    M, K = 256, 4096
+    blocks, _ = _weights(91, M, K)
+    x = (rng.standard_normal(K) * 2.0 ** rng.integers(-20, 21, K)).astype(np.float32)
+    big = np.argsort(-np.abs(x).reshape(-1, 32), axis=1)[:, 0] + 32 * np.arange(K // 32)
+    for m in range(0, M, 2):  # even rows: weight 0 (nibble 8) at each block's largest |x|
+        for c in big:
+            b, j = divmod(int(c), 32)
+            byte = 2 + (j % 16)
+            blocks[m, b, byte] = (blocks[m, b, byte] & (0x0F if j >= 16 else 0xF0)) | ((8 << 4) if j >= 16 else 8)
+    y = _gguf_matvec(hip, "q4", blocks, x)
+    worst = assert_matvec_close(y, oracle.matmul_q4_0_gguf(blocks, x, NT), oracle.dequantize_q4_0(blocks), x)
+    assert worst < 1e-6
+
+
+def test_forcing_mfma_on_an_ineligible_shape_is_an_error(hip, q4_kernel):
+    q4_kernel(native.Q4_KERNEL_MFMA)
+    blocks, x = _weights(8, 16, 96)
+    db, dx, dy = DeviceBuffer.from_numpy(blocks), DeviceBuffer.from_numpy(x), DeviceBuffer(16 * 4)
+    assert hip.asmhip_matmul_q4_0(db.ptr, dx.ptr, dy.ptr, 16, 96, None) == native.ERR_UNSUPPORTED
+    assert "MFMA" in hip.asmhip_last_error().decode()
+    assert hip.asmhip_set_q4_kernel(7) == -1
+
+
+# ---- fused pre-ops and accumulation ---------------------------------------------------------
+
+def _fused(hip, qtype, blocks, x, pre, arg, eps, y0):
+    M, K = blocks.shape[0], blocks.shape[1] * 32
+    db, dx = DeviceBuffer.from_numpy(blocks), DeviceBuffer.from_numpy(x)
+    da = DeviceBuffer.from_numpy(arg) if arg is not None else None
+    dy = DeviceBuffer.from_numpy(y0) if y0 is not None else DeviceBuffer(M * 4)
+    rc = hip.asmhip_matmul_fused(qtype, db.ptr, dx.ptr, dy.ptr, M, K, pre, da.ptr if da else None, eps,
+                                 int(y0 is not None), None)
+    assert rc == 0, hip.asmhip_last_error()
+    synchronize()
+    return dy.download(np.float32, M)
+
+
+@pytest.mark.parametrize("qt,kernel", [("q4", native.Q4_KERNEL_FP32), ("q4", native.Q4_KERNEL_MFMA),
+                                       ("q8", native.Q4_KERNEL_AUTO)], ids=["q4-fp32", "q4-mfma", "q8"])
+@pytest.mark.parametrize("pre", ["none", "rmsnorm", "swiglu"])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_fused_matvec(hip, oracle, q4_kernel, qt, kernel, pre, accumulate):
+    q4_kernel(kernel)
+    M, K = 1000, 4096 if pre != "swiglu" else 11008
+    blocks, x = _weights(17 + K, M, K, qt)
+    rng = np.random.default_rng(5)
+    arg = None
+    x_eff = x
+    if pre == "rmsnorm":
+        arg = rng.uniform(0.5, 1.5, K).astype(np.float32)
+        x_eff = oracle.rmsnorm(x, arg, 1e-6)
+    elif pre == "swiglu":
+        arg = rng.standard_normal(K).astype(np.float32)
+        x_eff = oracle.silu_hadamard(x, arg)
+    y0 = rng.standard_normal(M).astype(np.float32) if accumulate else None
+    code = {"none": native.PRE_NONE, "rmsnorm": native.PRE_RMSNORM, "swiglu": native.PRE_SWIGLU}[pre]
+    y = _fused(hip, native.Q4_0 if qt == "q4" else native.Q8_0, blocks, x, code, arg, 1e-6, y0)
+    if qt == "q4":
+        ref, w = oracle.matmul_q4_0_gguf(blocks, x_eff, NT), oracle.dequantize_q4_0(blocks)
+    else:
+        ref, w = oracle.matmul_q8_0_gguf(blocks, x_eff, NT), oracle.dequantize_q8_0(blocks)
+    if accumulate:
+        ref = ref + y0
+        # the residual's own rounding: half an ulp of |y0| on top of the matvec bar
+        l1 = np.abs(w.astype(np.float64)) @ np.abs(x_eff.astype(np.float64))
+        err = np.abs(y.astype(np.float64) - ref.astype(np.float64))
+        assert np.all(err <= 1e-4 * l1 + 2.0 ** -23 * np.abs(ref.astype(np.float64)))
+    else:
+        assert_matvec_close(y, ref, w, x_eff)
+
+
+def test_fused_pre_op_needs_its_argument(hip):
+    blocks, x = _weights(9, 16, 4096)
+    db, dx, dy = DeviceBuffer.from_numpy(blocks), DeviceBuffer.from_numpy(x), DeviceBuffer(16 * 4)
+    assert hip.asmhip_matmul_fused(native.Q4_0, db.ptr, dx.ptr, dy.ptr, 16, 4096, native.PRE_RMSNORM, None,
+                                   1e-6, 0, None) == -1
+    assert hip.asmhip_matmul_fused(5, db.ptr, dx.ptr, dy.ptr, 16, 4096, 0, None, 0.0, 0, None) == -1
