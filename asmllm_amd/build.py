@@ -35,6 +35,8 @@ ARCH = "gfx950"
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-std=c++17",
     "-fPIC",
     "-fvisibility=hidden",

@@ -24,12 +24,20 @@
 // inside one 32-block.  Every instruction above runs once per MFMA whichever
 // level a lane holds, so the second level costs only x preparation and LDS.
 //
-// Work mapping: a workgroup of 4 waves owns 16 rows; the waves take K in
-// 16-block chunks round robin.  A wave streams a chunk (16 rows x 288 bytes)
-// with coalesced 16-byte buffer loads, two chunks in flight, parks it in LDS
-// and reads the MFMA operands back.  x is digitized once per workgroup into
-// LDS; its loads are issued before the weight loads (loads retire in order),
-// so the digit work waits on x only and overlaps the weight stream.
+// Work mapping (persistent stream): one workgroup of NW waves per compute
+// unit.  Workgroup b owns the 16-row tiles b, b + G, b + 2G, ... (G = grid
+// size); a tile's K is cut into 8-block units (16 rows x 144 bytes), and wave w
+// takes units w, w + NW, ... of every tile in turn, so each wave walks one long
+// sequence of units.  D units of loads stay in flight per wave (coalesced
+// 16-byte buffer loads; past the end of the sequence the offset is pushed
+// beyond the buffer, which returns zeros without touching memory).  A unit is
+// parked in the wave's LDS slot and its MFMA operands are read back.  x is
+// digitized once per workgroup into LDS while the first loads are in flight.
+// Each wave keeps its per-tile partial sums in LDS; after the stream the
+// workgroup adds the NW partials of every row in a fixed order.  The main
+// loop has no workgroup barrier.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -39,16 +47,17 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
-constexpr int kThreadsM = kWaves * kWave;
-constexpr int kCB = 16;                      // blocks per chunk
-constexpr int kPitch = 304;                  // LDS bytes per staged row: 16 x 18 = 288 used, 16-aligned
-constexpr int kWBuf = 16 * kPitch;           // LDS bytes per wave
-constexpr int kXBlk = 256;                   // LDS bytes of x digits per block: [g][level*4+digit][8]
-constexpr int kPieces = 16 * kCB * 18 / 16;  // 16-byte pieces per chunk (288)
-constexpr int kMaxBlocks = 512;              // K <= 16384
+constexpr int kUnitBlocks = 8;                     // blocks per unit
+constexpr int kUnitRowBytes = kUnitBlocks * 18;    // 144: one row's slice of a unit
+constexpr int kUnitBytes = 16 * kUnitRowBytes;     // 2304: LDS slot per wave
+constexpr int kUnitPieces = kUnitBytes / 16;       // 144 16-byte pieces: 3 loads per lane
+constexpr int kXStride = 264;                      // LDS bytes of x digits per block: [g][level*4+digit][8] + 8 pad
+                                                   // (the pad staggers blocks across banks: conflict-free 8-byte writes)
+constexpr int kMaxBlocks = 512;                    // K <= 16384
+constexpr int kMaxTilesPerGroup = 8;
+constexpr uint32_t kPastEnd = 0xFFFFFF00u;         // buffer offset that loads zeros
 
-static_assert(kPieces <= 5 * kWave, "a chunk is five 16-byte loads per lane");
+static_assert(kUnitPieces <= 3 * 64, "a unit is three 16-byte loads per lane");
 
 __device__ __forceinline__ long pack_q4(uint32_t q) {
     const uint32_t lo = ((q << 4) ^ 0x80808080u) & 0xF0F0F0F0u;  // bytes 16 (n_lo - 8)
@@ -83,220 +92,315 @@ __device__ __forceinline__ float block_value(v4i d) {
     return fmaf((float)hi, 65536.0f, (float)lo);
 }
 
-template <int XQ>
-__global__ __launch_bounds__(kThreadsM) void q4_0_mfma_kernel(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                              float* __restrict__ y, int M, int K, int pre,
-                                                              const float* __restrict__ pre_arg, float eps,
-                                                              int accumulate) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ float red[kWaves];
-    const int nb = K >> 5;
-    const int nch = (nb + kCB - 1) / kCB;
-    const uint32_t row_bytes = (uint32_t)nb * 18u;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
-    const int row0 = blockIdx.x * 16;
-    const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
-    uint8_t* wbuf = lds + wave * kWBuf;
-    uint8_t* xdig = lds + kWaves * kWBuf;
-    float* xscale = reinterpret_cast<float*>(xdig + nb * kXBlk);
-    float* part = xscale + nb;
+// Row n's dot with x over NB staged blocks (NB even), for the lane (n, g):
+// every operand is read from LDS first, then the MFMAs issue back to back,
+// then the per-block epilogues; no branch separates them.
+template <int NB>
+__device__ __forceinline__ float chunk_dot(const uint8_t* rowd, const uint8_t* rowp, const uint8_t* xa,
+                                           const float* xs, float acc) {
+    constexpr int NP = NB / 2;
+    long bq[NB], aq[NB];
+    uint32_t sc[NP][2];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        // blocks 2p (bytes 36p..) and 2p+1 (bytes 36p+18..) of row n
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(rowp + 36 * p);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(rowp + 36 * p + 4);
+        const uint32_t w5 = *reinterpret_cast<const uint32_t*>(rowp + 36 * p + 20);
+        bq[2 * p] = pack_q4(__builtin_amdgcn_alignbyte(w1, w0, 2));
+        bq[2 * p + 1] = pack_q4(w5);
+        // fp16 scales of the two blocks (low half, high half); the same for every lane group
+        sc[p][0] = *reinterpret_cast<const uint32_t*>(rowd + 36 * p);
+        sc[p][1] = *reinterpret_cast<const uint32_t*>(rowd + 36 * p + 16);
+        aq[2 * p] = *reinterpret_cast<const long*>(xa + (2 * p) * kXStride);
+        aq[2 * p + 1] = *reinterpret_cast<const long*>(xa + (2 * p + 1) * kXStride);
+    }
+    const v4i z = {0, 0, 0, 0};
+    v4i d[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) d[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq[j], bq[j], z, 0, 0, 0);
+    float acc1 = 0.f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        acc = fmaf(block_value(d[2 * p]) * xs[2 * p], half_lo(sc[p][0]), acc);
+        acc1 = fmaf(block_value(d[2 * p + 1]) * xs[2 * p + 1], half_hi(sc[p][1]), acc1);
+    }
+    return acc + acc1;
+}
 
-    // 1) x (and the pre-op argument) first.
-    const int nq = nb * 8;
-    float4 xv[XQ], av[XQ];
+template <int XQ, int NW, int D>
+__global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __restrict__ w,
+                                                            const float* __restrict__ x, float* __restrict__ y,
+                                                            int M, int K, int pre, const float* __restrict__ pre_arg,
+                                                            float eps, int accumulate) {
+    constexpr int kThreads = NW * 64;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float red[NW];
+    const int nb = K >> 5;
+    const int nu = nb / kUnitBlocks;  // units per tile
+    const uint32_t row_bytes = (uint32_t)nb * 18u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int G = gridDim.x;
+    const int n_tiles = (M + 15) >> 4;
+    const int my_tiles = (n_tiles - (int)blockIdx.x + G - 1) / G;
+    const int per_w = wave < nu ? (nu - wave + NW - 1) / NW : 0;  // this wave's units per tile
+    const int L = my_tiles * per_w;                              // length of this wave's stream
+    const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
+    uint8_t* wbuf = lds + wave * kUnitBytes;
+    uint8_t* xdig = lds + NW * kUnitBytes;
+    float* xscale = reinterpret_cast<float*>(xdig + nb * kXStride);
+    float* part = xscale + nb;  // [my_tiles][NW][16]
+
+    // This lane's three 16-byte pieces of a unit: piece q = row q / 9, bytes
+    // 16 (q % 9) of the row's 144-byte slice.  Rows past M fall beyond the
+    // buffer and load zeros.
+    uint32_t poff[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int q = min(lane + 64 * k, kUnitPieces - 1);
+        poff[k] = (uint32_t)(q / 9) * row_bytes + 16u * (uint32_t)(q % 9);
+    }
+    // unit s of the stream -> (tile slot i, unit u)
+    auto load_unit = [&](uint4* buf, int s) {
+        const int i = s / max(per_w, 1);
+        const int u = wave + NW * (s - i * per_w);
+        const uint32_t base = s < L ? (uint32_t)(((int)blockIdx.x + G * i) * 16) * row_bytes + (uint32_t)u * kUnitRowBytes
+                                    : kPastEnd;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) buf[k] = buf_load_b128(wr, s < L ? base + poff[k] : kPastEnd);
+    };
+
+    // 1) x (and the pre-op argument) first.  Item it = (block it / 4, k-group
+    // g = it % 4): x[32b + 4g .. +3] and x[32b + 16 + 4g .. +3], the 8 positions
+    // of one A-operand lane.
+    const int ni = nb * 4;
+    float4 xv[XQ][2], av[XQ][2];
 #pragma unroll
     for (int i = 0; i < XQ; ++i) {
-        const int qi = min((int)threadIdx.x + kThreadsM * i, nq - 1);
-        xv[i] = *reinterpret_cast<const float4*>(x + 4 * qi);
-        if (pre != kPreNone) av[i] = *reinterpret_cast<const float4*>(pre_arg + 4 * qi);
+        const int it = min((int)threadIdx.x + kThreads * i, ni - 1);
+        const int off = 32 * (it >> 2) + 4 * (it & 3);
+        xv[i][0] = *reinterpret_cast<const float4*>(x + off);
+        xv[i][1] = *reinterpret_cast<const float4*>(x + off + 16);
+        if (pre != kPreNone) {
+            av[i][0] = *reinterpret_cast<const float4*>(pre_arg + off);
+            av[i][1] = *reinterpret_cast<const float4*>(pre_arg + off + 16);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2) this wave's first two chunks (chunk index and row clamped; every load issued).
-    uint4 b0[5], b1[5];
-    auto load_chunk = [&](uint4* buf, int c) {
-        c = min(c, nch - 1);
+    // 2) the first D units of this wave's stream.
+    uint4 buf[D][3];
 #pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const int q = min(lane + kWave * i, kPieces - 1);
-            const int n = q / 18, p = q - n * 18;
-            const int row = min(row0 + n, M - 1);
-            buf[i] = buf_load_b128(wr, (uint32_t)row * row_bytes + (uint32_t)c * (kCB * 18) + 16u * p);
-        }
-    };
-    int c = wave;
-    load_chunk(b0, c);
-    load_chunk(b1, c + kWaves);
+    for (int d = 0; d < D; ++d) load_unit(buf[d], d);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3) fused pre-op on x, then digits.
+    // 3) fused pre-op on x, then digits; partial sums start at zero.
+    for (int i = threadIdx.x; i < my_tiles * NW * 16; i += kThreads) part[i] = 0.f;
     if (pre == kPreRmsNorm) {
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < XQ; ++i)
-            if ((int)threadIdx.x + kThreadsM * i < nq) {
-                ss = fmaf(xv[i].x, xv[i].x, ss);
-                ss = fmaf(xv[i].y, xv[i].y, ss);
-                ss = fmaf(xv[i].z, xv[i].z, ss);
-                ss = fmaf(xv[i].w, xv[i].w, ss);
+            if ((int)threadIdx.x + kThreads * i < ni) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    ss = fmaf(xv[i][h].x, xv[i][h].x, ss);
+                    ss = fmaf(xv[i][h].y, xv[i][h].y, ss);
+                    ss = fmaf(xv[i][h].z, xv[i][h].z, ss);
+                    ss = fmaf(xv[i][h].w, xv[i][h].w, ss);
+                }
             }
         ss = wave_sum(ss);
         if (lane == 0) red[wave] = ss;
         __syncthreads();
-        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+        float tot = 0.f;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) tot += red[k];
         const float inv = 1.0f / sqrtf(tot / (float)K + eps);
 #pragma unroll
-        for (int i = 0; i < XQ; ++i) {
-            xv[i].x = __fmul_rn(__fmul_rn(xv[i].x, inv), av[i].x);
-            xv[i].y = __fmul_rn(__fmul_rn(xv[i].y, inv), av[i].y);
-            xv[i].z = __fmul_rn(__fmul_rn(xv[i].z, inv), av[i].z);
-            xv[i].w = __fmul_rn(__fmul_rn(xv[i].w, inv), av[i].w);
-        }
+        for (int i = 0; i < XQ; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                xv[i][h].x = __fmul_rn(__fmul_rn(xv[i][h].x, inv), av[i][h].x);
+                xv[i][h].y = __fmul_rn(__fmul_rn(xv[i][h].y, inv), av[i][h].y);
+                xv[i][h].z = __fmul_rn(__fmul_rn(xv[i][h].z, inv), av[i][h].z);
+                xv[i][h].w = __fmul_rn(__fmul_rn(xv[i][h].w, inv), av[i][h].w);
+            }
     } else if (pre == kPreSwiGlu) {
 #pragma unroll
-        for (int i = 0; i < XQ; ++i) {
-            xv[i].x = __fmul_rn(xv[i].x / (1.0f + expf(-xv[i].x)), av[i].x);
-            xv[i].y = __fmul_rn(xv[i].y / (1.0f + expf(-xv[i].y)), av[i].y);
-            xv[i].z = __fmul_rn(xv[i].z / (1.0f + expf(-xv[i].z)), av[i].z);
-            xv[i].w = __fmul_rn(xv[i].w / (1.0f + expf(-xv[i].w)), av[i].w);
-        }
+        for (int i = 0; i < XQ; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                xv[i][h].x = __fmul_rn(xv[i][h].x / (1.0f + expf(-xv[i][h].x)), av[i][h].x);
+                xv[i][h].y = __fmul_rn(xv[i][h].y / (1.0f + expf(-xv[i][h].y)), av[i][h].y);
+                xv[i][h].z = __fmul_rn(xv[i][h].z / (1.0f + expf(-xv[i][h].z)), av[i][h].z);
+                xv[i][h].w = __fmul_rn(xv[i][h].w / (1.0f + expf(-xv[i][h].w)), av[i][h].w);
+            }
     }
 #pragma unroll
     for (int i = 0; i < XQ; ++i) {
-        const int qi = (int)threadIdx.x + kThreadsM * i;
-        const float4 v = xv[i];
-        // the 8 quads of a block sit in 8 consecutive lanes
-        float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        mx = fmaxf(mx, __shfl_xor(mx, 1, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 4, kWave));
+        const int it = (int)threadIdx.x + kThreads * i;
+        const float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                            xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+        // the 4 items of a block sit in 4 consecutive lanes
+        float mx = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) mx = fmaxf(mx, fabsf(v[t]));
+        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
         int e;
         frexpf(mx, &e);  // mx < 2^e (e = 0 for mx = 0)
         e = max(e, -60);
         const float sc = ldexpf(1.0f, 30 - e);
-        const float f[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};  // exact: power-of-two scaling, |f| < 2^30
-        uint32_t Y1[4], Y2[4];
+        uint32_t Y1[8], Y2[8];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const float tr = truncf(f[t]);
+        for (int t = 0; t < 8; ++t) {
+            const float f = v[t] * sc;  // exact: power-of-two scaling, |f| < 2^30
+            const float tr = truncf(f);
             Y1[t] = digit_word((int)tr);
-            Y2[t] = digit_word((int)((f[t] - tr) * 1073741824.0f));  // fraction exact; 2^30
+            Y2[t] = digit_word((int)((f - tr) * 1073741824.0f));  // fraction exact; 2^30
         }
-        uint32_t d1[4], d2[4];
-        transpose_digits(Y1, d1);
-        transpose_digits(Y2, d2);
-        if (qi < nq) {
-            // quad qq holds x[4qq .. 4qq+3] of block b: k-group qq & 3, half qq >> 2
-            const int b = qi >> 3, qq = qi & 7;
-            uint8_t* base = xdig + b * kXBlk + (qq & 3) * 64 + (qq >> 2) * 4;
+        uint32_t d1l[4], d1h[4], d2l[4], d2h[4];
+        transpose_digits(Y1, d1l);
+        transpose_digits(Y1 + 4, d1h);
+        transpose_digits(Y2, d2l);
+        transpose_digits(Y2 + 4, d2h);
+        if (it < ni) {
+            // row r of this lane's A operand: 8 bytes at g * 64 + 8 r; rows 0-3 X1, 4-7 X2, top digit first
+            const int b = it >> 2, g = it & 3;
+            uint64_t* base = reinterpret_cast<uint64_t*>(xdig + b * kXStride + g * 64);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                *reinterpret_cast<uint32_t*>(base + 8 * k) = d1[3 - k];       // rows 0-3: X1, top digit first
-                *reinterpret_cast<uint32_t*>(base + 32 + 8 * k) = d2[3 - k];  // rows 4-7: X2
+                base[k] = ((uint64_t)d1h[3 - k] << 32) | d1l[3 - k];
+                base[4 + k] = ((uint64_t)d2h[3 - k] << 32) | d2l[3 - k];
             }
-            if (qq == 0) xscale[b] = ldexpf(1.0f, e - 34);  // 2^(e-30) for X1, 1/16 for the weight bytes
+            if (g == 0) xscale[b] = ldexpf(1.0f, e - 34);  // 2^(e-30) for X1, 1/16 for the weight bytes
         }
     }
     __syncthreads();
 
-    // 4) MFMA over this wave's chunks.
+    // 4) the stream: stage unit s, multiply, refill its buffer with unit s + D.
     const int n = lane & 15, g = lane >> 4;
     const int aoff = g * 64 + (n & 7) * 8;
-    const uint8_t* rowd = wbuf + n * kPitch;  // row n's staged blocks (scales at 18 j)
-    const uint8_t* rowp = rowd + 4 * g;       // this lane's qs dword
+    const uint8_t* rowd = wbuf + n * kUnitRowBytes;  // row n's staged blocks (scales at 18 j)
+    const uint8_t* rowp = rowd + 4 * g;              // this lane's qs dword
     float acc = 0.f;
-    auto compute = [&](const uint4* buf, int cc) {
+    for (int s0 = 0; s0 < L; s0 += D) {
 #pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const int q = lane + kWave * i;
-            if (q < kPieces) {
-                const int r = q / 18, p = q - r * 18;
-                *reinterpret_cast<uint4*>(wbuf + r * kPitch + 16 * p) = buf[i];
+        for (int d = 0; d < D; ++d) {
+            const int s = s0 + d;
+            if (s < L) {
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    const int q = lane + 64 * k;
+                    if (q < kUnitPieces) *reinterpret_cast<uint4*>(wbuf + 16 * q) = buf[d][k];
+                }
+                __builtin_amdgcn_wave_barrier();
+                const int i = s / per_w;
+                const int u = wave + NW * (s - i * per_w);
+                acc = chunk_dot<kUnitBlocks>(rowd, rowp, xdig + u * kUnitBlocks * kXStride + aoff,
+                                             xscale + u * kUnitBlocks, acc);
+                __builtin_amdgcn_wave_barrier();
+                load_unit(buf[d], s + D);
+                if (s - i * per_w == per_w - 1) {  // last unit of tile slot i
+                    const float acc2 = __shfl_down(acc, 16, 64);  // level 2 of row n
+                    if (g == 0) part[(i * NW + wave) * 16 + n] = fmaf(acc2, 9.313225746154785e-10f, acc);  // 2^-30
+                    acc = 0.f;
+                }
             }
         }
-        __builtin_amdgcn_wave_barrier();
-        const int nbk = min(kCB, nb - cc * kCB);  // even: nb % 8 == 0
-        const v4i z = {0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < kCB; j += 2) {
-            if (j < nbk) {
-                // blocks j (bytes 18j..) and j+1 (bytes 18j+18..) of row n
-                const uint32_t w0 = *reinterpret_cast<const uint32_t*>(rowp + 18 * j);
-                const uint32_t w1 = *reinterpret_cast<const uint32_t*>(rowp + 18 * j + 4);
-                const uint32_t w5 = *reinterpret_cast<const uint32_t*>(rowp + 18 * j + 20);
-                // fp16 scales of blocks j (low half) and j+1 (high half), the same for every lane group
-                const uint32_t sA = *reinterpret_cast<const uint32_t*>(rowd + 18 * j);
-                const uint32_t sB = *reinterpret_cast<const uint32_t*>(rowd + 18 * j + 16);
-                const int jb = cc * kCB + j;
-                const long aA = *reinterpret_cast<const long*>(xdig + jb * kXBlk + aoff);
-                const long aB = *reinterpret_cast<const long*>(xdig + (jb + 1) * kXBlk + aoff);
-                const v4i dA = __builtin_amdgcn_mfma_i32_16x16x32_i8(aA, pack_q4(__builtin_amdgcn_alignbyte(w1, w0, 2)),
-                                                                     z, 0, 0, 0);
-                const v4i dB = __builtin_amdgcn_mfma_i32_16x16x32_i8(aB, pack_q4(w5), z, 0, 0, 0);
-                acc = fmaf(block_value(dA) * xscale[jb], half_lo(sA), acc);
-                acc = fmaf(block_value(dB) * xscale[jb + 1], half_hi(sB), acc);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-    };
-    while (c < nch) {
-        compute(b0, c);
-        const int c2 = c + kWaves;
-        if (c2 < nch) {
-            if (c2 + kWaves < nch) load_chunk(b0, c2 + kWaves);
-            compute(b1, c2);
-            if (c2 + 2 * kWaves < nch) load_chunk(b1, c2 + 2 * kWaves);
-        }
-        c = c2 + kWaves;
     }
-
-    // 5) combine the waves' partial sums in a fixed order.
-    const float acc2 = __shfl_down(acc, 16, kWave);  // level 2 of row n
-    if (g == 0) part[wave * 16 + n] = fmaf(acc2, 9.313225746154785e-10f, acc);  // 2^-30
     __syncthreads();
-    if (wave == 0 && lane < 16 && row0 + lane < M) {
-        const float s = (part[lane] + part[16 + lane]) + (part[32 + lane] + part[48 + lane]);
-        y[row0 + lane] = accumulate ? y[row0 + lane] + s : s;
+
+    // 5) add the waves' partial sums of every row in a fixed order.
+    for (int idx = threadIdx.x; idx < my_tiles * 16; idx += kThreads) {
+        const int i = idx >> 4, r = idx & 15;
+        const int row = ((int)blockIdx.x + G * i) * 16 + r;
+        if (row < M) {
+            float sum = 0.f;
+#pragma unroll
+            for (int k = 0; k < NW; ++k) sum += part[(i * NW + k) * 16 + r];
+            y[row] = accumulate ? y[row] + sum : sum;
+        }
     }
 }
 
+constexpr int kStreamWaves = 8;
+constexpr int kStreamDepth = 2;
+
 template <int XQ>
-int launch_xq(const uint8_t* w, const float* x, float* y, int M, int K, size_t lds, hipStream_t st,
+int launch_xq(const uint8_t* w, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
-    const int rc = dynamic_lds((const void*)q4_0_mfma_kernel<XQ>, lds);
+    const void* fn = (const void*)q4_0_mfma_stream<XQ, kStreamWaves, kStreamDepth>;
+    const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
-    hipLaunchKernelGGL((q4_0_mfma_kernel<XQ>), dim3((M + 15) / 16), dim3(kThreadsM), lds, st, w, x, y, M, K, o.pre,
-                       o.pre_arg, o.eps, (int)o.accumulate);
+    hipLaunchKernelGGL((q4_0_mfma_stream<XQ, kStreamWaves, kStreamDepth>), dim3(grid), dim3(kStreamWaves * 64), lds,
+                       st, w, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate);
     return kOk;
 }
 
-size_t mfma_lds_bytes(int nb) { return (size_t)kWaves * kWBuf + (size_t)nb * (kXBlk + 4) + kWaves * 16 * 4; }
+// Workgroup layout of one launch: grid size, tiles per workgroup, LDS bytes.
+struct StreamShape {
+    int grid, tiles_per_group;
+    size_t lds;
+};
+
+int compute_units();
+
+StreamShape stream_shape(int64_t M, int64_t K) {
+    const int nb = (int)(K / 32);
+    const int n_tiles = (int)((M + 15) / 16);
+    StreamShape sh;
+    sh.grid = std::max(std::min(n_tiles, compute_units()), (n_tiles + kMaxTilesPerGroup - 1) / kMaxTilesPerGroup);
+    sh.tiles_per_group = (n_tiles + sh.grid - 1) / sh.grid;
+    sh.lds = (size_t)kStreamWaves * kUnitBytes + (size_t)nb * (kXStride + 4) +
+             (size_t)sh.tiles_per_group * kStreamWaves * 16 * sizeof(float);
+    return sh;
+}
+
+int compute_units() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+            (void)hipGetLastError();
+            n = 256;
+        }
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
 
 }  // namespace
 
 bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& o, int64_t M, int64_t K) {
     const int64_t nb = K / 32;
-    return K % 256 == 0 && nb >= 8 && nb <= kMaxBlocks && M >= 1 && M * nb * 18 < (int64_t)UINT32_MAX &&
-           (uintptr_t)w % 4 == 0 && (uintptr_t)x % 16 == 0 &&
-           (o.pre == kPreNone || (uintptr_t)o.pre_arg % 16 == 0);
+    return K % 256 == 0 && nb >= kUnitBlocks && nb <= kMaxBlocks && M >= 1 && M <= INT32_MAX - 16 &&
+           (M + 16) * nb * 18 < (int64_t)kPastEnd && (uintptr_t)w % 4 == 0 && (uintptr_t)x % 16 == 0 &&
+           (o.pre == kPreNone || (uintptr_t)o.pre_arg % 16 == 0) &&
+           stream_shape(M, K).lds + 256 <= 160 * 1024;
 }
 
 int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st,
                      const MatvecOpts& o) {
     const int nb = (int)(K / 32);
-    const int xq = (nb * 8 + kThreadsM - 1) / kThreadsM;  // quads of x per thread
-    const size_t lds = mfma_lds_bytes(nb);
+    const StreamShape sh = stream_shape(M, K);
+    const int grid = sh.grid;
+    const size_t lds = sh.lds;
+    const int xq = (nb * 4 + kStreamWaves * 64 - 1) / (kStreamWaves * 64);  // x items (8 positions) per thread
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const int m = (int)M, k = (int)K;
     int rc;
-    if (xq <= 4)
-        rc = launch_xq<4>(wb, x, y, m, k, lds, st, o);
-    else if (xq <= 8)
-        rc = launch_xq<8>(wb, x, y, m, k, lds, st, o);
-    else if (xq <= 12)
-        rc = launch_xq<12>(wb, x, y, m, k, lds, st, o);
+    if (xq <= 1)
+        rc = launch_xq<1>(wb, x, y, m, k, grid, lds, st, o);
+    else if (xq <= 2)
+        rc = launch_xq<2>(wb, x, y, m, k, grid, lds, st, o);
     else
-        rc = launch_xq<16>(wb, x, y, m, k, lds, st, o);
+        rc = launch_xq<4>(wb, x, y, m, k, grid, lds, st, o);  // nb <= 512: at most 4 items per thread
     if (rc) return rc;
     ASMHIP_TRY(hipGetLastError());
     return kOk;
