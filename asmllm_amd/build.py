@@ -28,6 +28,7 @@ SOURCES = [
     "matvec_mfma.hip",
     "decode_ops.hip",
     "quant.hip",
+    "gemm.hip",
     "capi.hip",
 ]
 

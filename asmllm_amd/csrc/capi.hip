@@ -447,6 +447,12 @@ extern "C" int asmhip_matmul_fused(int qtype, const void* blocks, const float* x
     return matvec_launch(qt, true, blocks, nullptr, x, y, M, K, (hipStream_t)stream, o);
 }
 
+extern "C" int asmhip_gemm_q8_0(const void* w_blocks, const void* a_blocks, float* c, int64_t T, int64_t M,
+                                int64_t K, void* stream) {
+    int rc = check_ptrs(w_blocks, a_blocks, c);
+    return rc ? rc : gemm_q8_0_launch(w_blocks, a_blocks, c, T, M, K, (hipStream_t)stream);
+}
+
 extern "C" int asmhip_set_q4_kernel(int kernel) { return set_q4_kernel(kernel); }
 extern "C" int asmhip_get_q4_kernel(void) { return get_q4_kernel(); }
 

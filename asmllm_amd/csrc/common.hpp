@@ -51,6 +51,10 @@ __device__ __forceinline__ uint2 buf_load_b64(__amdgpu_buffer_rsrc_t r, uint32_t
     return make_uint2(v[0], v[1]);
 }
 
+__device__ __forceinline__ uint32_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
 __device__ __forceinline__ uint32_t buf_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }

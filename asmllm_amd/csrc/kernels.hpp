@@ -42,6 +42,10 @@ bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& opts, i
 int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t stream,
                      const MatvecOpts& opts);
 
+// C[T][M] = A (Q8_0 blocks [T][K/32]) x W (Q8_0 blocks [M][K/32])^T, block dots
+// scaled by both fp16 scales and accumulated in block order.
+int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t M, int64_t K, hipStream_t stream);
+
 // Exact fp32 dequantization of GGUF blocks, row-major [rows][K].
 int dequant_launch(QuantType qt, const void* w, float* out, int64_t rows, int64_t K, hipStream_t stream);
 

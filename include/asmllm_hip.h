@@ -132,6 +132,13 @@ ASMHIP_API int asmhip_dequantize_q8_0(const void* blocks, float* w, int64_t rows
  * != 0 adds W x into y (the residual add) instead of overwriting y. */
 ASMHIP_API int asmhip_matmul_fused(int qtype, const void* blocks, const float* x, float* y, int64_t M, int64_t K,
                                    int pre_op, const float* pre_arg, float eps, int accumulate, void* stream);
+/* Prefill GEMM: C[T][M] = sum over blocks b of int32 dot(A[t,b], W[j,b]) * d_w[j,b] * d_a[t,b],
+ * accumulated in fp32 in block order; A = T activation rows and W = M weight rows, both
+ * Q8_0 blocks [rows][K/32] (quantize activations with asmhip_quantize(ASMHIP_Q8_0, ...)).
+ * The reference's only quantized-activation recipe (matmul_q4_neon.S:57-143, 190-255)
+ * applied to a batch; the reference itself has no GEMM. */
+ASMHIP_API int asmhip_gemm_q8_0(const void* w_blocks, const void* a_blocks, float* c, int64_t T, int64_t M,
+                                int64_t K, void* stream);
 /* Process-wide Q4_0 GGUF kernel choice (ASMHIP_Q4_KERNEL_*). */
 ASMHIP_API int asmhip_set_q4_kernel(int kernel);
 ASMHIP_API int asmhip_get_q4_kernel(void);
