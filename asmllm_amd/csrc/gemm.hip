@@ -6,24 +6,28 @@
 // (fp16 d + 32 int8); C is fp32 [T][M].  The semantics are those of the
 // reference's quantized-activation recipe (int32 block dot, scvtf, product of
 // the two scales, fmadd: src/kernels/arm64/matmul_q4_neon.S:190-255), applied
-// block by block in order.
+// block by block in order; the result is bitwise that of the CPU oracle.
 //
 // Per 32x32 output tile and block, two matrix instructions and two VALU ones:
 //   v_mfma_i32_32x32x32_i8   the exact int32 block dots;
-//   v_mfma_f32_32x32x2_f32   the outer product d_a (x) d_w of the block scales
-//                            (K = 2 with the second slice zero), which lands in
-//                            the same lane/register layout as the dots;
-//   v_cvt_f32_i32 + v_fma    acc += float(dot) * scale, in block order.
-// The scale product on the matrix pipe keeps the VALU at two instructions per
-// output and block (the bound of this GEMM: every output needs its own scale
-// in every block).
+//   v_mfma_f32_32x32x8_f16   the outer product of the raw fp16 block scales
+//                            (each placed in both lane halves: 2 d_a d_w,
+//                            exact in fp32), in the same lane/register layout
+//                            as the dots;
+//   v_cvt_f32_i32 + v_fma    acc += float(dot) * 2 d_a d_w, in block order;
+// the result is halved (exactly) at the store.  The scale product on the
+// matrix pipe keeps the VALU at two instructions per output and block, the
+// bound of this GEMM: every output needs its own scale in every block.
 //
 // Work mapping: a workgroup of 4 waves computes a 64 (T) x 128 (M) tile; wave
-// (wt, wm) owns rows 32 wt.. and columns 64 wm.. (two 32x32 tiles).  K goes in
-// steps of 4 blocks: the workgroup stages the step's 64 + 128 block rows in LDS
-// with qs realigned to 32-byte rows (padded to 144 bytes: conflict-free 16-byte
-// operand reads) and scales widened to fp32, double-buffered, the next step's
-// global loads in flight during the current step's MFMAs.
+// (wt, wm) owns rows 32 wt.. and columns 64 wm.. (two 32x32 tiles).
+// Fast path (K % 64 == 0): K goes in steps of two blocks; a row's step is 68
+// contiguous bytes, fetched with 16-byte loads by consecutive lanes and parked
+// raw in LDS (row pitch an odd number of dwords: conflict-free operand reads),
+// double-buffered with the next step's loads in flight.  Other K: blocks are
+// staged one by one with qs realigned on the way into LDS.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -34,28 +38,33 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr int kTT = 64;            // T rows per workgroup
 constexpr int kTM = 128;           // M columns per workgroup
-constexpr int kKB = 4;             // blocks per K step
-constexpr int kPitch = kKB * 32 + 16;  // LDS bytes per staged row of qs
 constexpr int kThreadsG = 256;
-constexpr int kStageBlocks = (kTT + kTM) * kKB;            // 768
-constexpr int kPerThread = kStageBlocks / kThreadsG;       // 3
 constexpr uint32_t kPastEnd = 0xFFFFFF00u;
-// LDS of one stage: qs of A and W rows, then their fp32 scales
-constexpr int kStageBytes = (kTT + kTM) * kPitch + (kTT + kTM) * kKB * 4;
 
-static_assert(kStageBlocks % kThreadsG == 0, "staging splits evenly");
+// Geometry of a K step of KB blocks.
+template <int KB>
+struct Step {
+    static constexpr int kPitch = KB * 32 + 16;                                   // LDS bytes per staged row of qs
+    static constexpr int kBlocks = (kTT + kTM) * KB;                              // blocks staged per step
+    static constexpr int kPerThread = (kBlocks + kThreadsG - 1) / kThreadsG;
+    static constexpr int kBytes = (kTT + kTM) * kPitch + (kTT + kTM) * KB * 4;    // qs rows, then fp32 scales
+};
 
 struct Staged {
     uint32_t dw[9];  // dwords covering the 32 qs bytes (the ninth: its low half only)
     uint32_t d16;    // the fp16 scale
 };
 
+template <int KB, bool kPipe>
 __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_kernel(const uint8_t* __restrict__ w,
                                                               const uint8_t* __restrict__ a,
                                                               float* __restrict__ c, int T, int M, int K) {
+    using S = Step<KB>;
+    constexpr int kKB = KB, kPitch = S::kPitch, kPerThread = S::kPerThread, kStageBytes = S::kBytes;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int nb = K >> 5;
     const uint32_t row_bytes = (uint32_t)nb * 34u;
@@ -71,6 +80,7 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_kernel(const uint8_t* __r
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
             const int ib = (int)threadIdx.x + kThreadsG * i;
+            if (ib >= S::kBlocks) break;  // wave-uniform
             const bool is_a = ib < kTT * kKB;
             const int local = is_a ? ib : ib - kTT * kKB;
             const int row = local / kKB, blk = local - row * kKB;
@@ -94,6 +104,7 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_kernel(const uint8_t* __r
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
             const int ib = (int)threadIdx.x + kThreadsG * i;
+            if (ib >= S::kBlocks) break;
             const bool is_a = ib < kTT * kKB;
             const int local = is_a ? ib : ib - kTT * kKB;
             const int row = local / kKB, blk = local - row * kKB;
@@ -129,8 +140,8 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_kernel(const uint8_t* __r
         const uint8_t* qs_base = stage;
         const float* sc_base = reinterpret_cast<const float*>(stage + (kTT + kTM) * kPitch);
         const int arow = 32 * wt + m;
-#pragma unroll 1
-        for (int blk = 0; blk < kKB; ++blk) {
+        // block blk, column tile nt: exact int32 dots and the scale outer product
+        auto issue = [&](int blk, v16i* dot, v16f* scl) {
             const v4i av = *reinterpret_cast<const v4i*>(qs_base + arow * kPitch + blk * 32 + 16 * g);
             const float da = g == 0 ? sc_base[arow * kKB + blk] : 0.f;
 #pragma unroll
@@ -140,10 +151,36 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_kernel(const uint8_t* __r
                 const float dw = g == 0 ? sc_base[wrow * kKB + blk] : 0.f;
                 const v16i zi = {};
                 const v16f zf = {};
-                const v16i dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zi, 0, 0, 0);
-                const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(da, dw, zf, 0, 0, 0);
+                dot[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zi, 0, 0, 0);
+                scl[nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(da, dw, zf, 0, 0, 0);
+            }
+        };
+        auto retire = [&](const v16i* dot, const v16f* scl) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[nt][i] = fmaf((float)dot[i], sc[i], acc[nt][i]);
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[nt][i] = fmaf((float)dot[nt][i], scl[nt][i], acc[nt][i]);
+        };
+        if (kPipe) {
+            // block b+1's matrix work is issued before block b's epilogue
+            v16i dot[2][2];
+            v16f scl[2][2];
+            issue(0, dot[0], scl[0]);
+#pragma unroll
+            for (int blk = 1; blk < kKB; ++blk) {
+                issue(blk, dot[blk & 1], scl[blk & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                retire(dot[(blk - 1) & 1], scl[(blk - 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            retire(dot[(kKB - 1) & 1], scl[(kKB - 1) & 1]);
+        } else {
+#pragma unroll 1
+            for (int blk = 0; blk < kKB; ++blk) {
+                v16i dot[2];
+                v16f scl[2];
+                issue(blk, dot, scl);
+                retire(dot, scl);
             }
         }
     }
@@ -161,6 +198,156 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_kernel(const uint8_t* __r
     }
 }
 
+// ---------------------------------------------------------------------------
+// Coalesced variant (K % 128 == 0): a step's K chunk of a row is KB * 34
+// contiguous bytes, fetched with 16-byte loads by consecutive lanes and parked
+// raw in LDS at a row pitch of an odd number of dwords (lanes of a 32-row
+// operand read land in distinct banks).  Operands are realigned as they are
+// read: qs of an even block start 2 bytes past a dword.
+// ---------------------------------------------------------------------------
+template <int KB>
+struct RawStep {
+    static constexpr int kChunk = KB * 34;                        // bytes of a row's K chunk
+    static constexpr int kPieces = (kChunk + 15) / 16;            // 16-byte loads per row
+    static constexpr int kPitch = ((kPieces * 16 / 4) | 1) * 4;   // odd number of dwords
+    static constexpr int kRows = kTT + kTM;
+    static constexpr int kTotal = kRows * kPieces;
+    static constexpr int kPerThread = (kTotal + kThreadsG - 1) / kThreadsG;
+    static constexpr int kBytes = kRows * kPitch;
+};
+
+// 16 qs bytes of block BLK (of a dword-aligned pair) for lane group g: an odd
+// block's qs are dword aligned, an even block's start 2 bytes past a dword
+template <int BLK>
+__device__ __forceinline__ v4i raw_qs(const uint8_t* row, int g) {
+    constexpr int off = 34 * BLK + 2;
+    const uint8_t* p = row + 16 * g;
+    if constexpr (off % 4 == 0) {
+        const uint32_t* d = reinterpret_cast<const uint32_t*>(p + off);
+        return v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+    } else {
+        const uint32_t* d = reinterpret_cast<const uint32_t*>(p + off - 2);
+        const uint32_t w0 = d[0], w1 = d[1], w2 = d[2], w3 = d[3], w4 = d[4];
+        return v4i{(int)__builtin_amdgcn_alignbyte(w1, w0, 2), (int)__builtin_amdgcn_alignbyte(w2, w1, 2),
+                   (int)__builtin_amdgcn_alignbyte(w3, w2, 2), (int)__builtin_amdgcn_alignbyte(w4, w3, 2)};
+    }
+}
+
+// A 32x32x8 f16 MFMA operand holding the block's raw fp16 scale in its first
+// half: with the scale in both lane halves of A and B, D = 2 d_a d_w exactly.
+template <int BLK>
+__device__ __forceinline__ v4h raw_scale(const uint8_t* row) {
+    v4h v = {};
+    v[0] = *reinterpret_cast<const _Float16*>(row + 34 * BLK);
+    return v;
+}
+
+template <int KB>
+__global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* __restrict__ w,
+                                                                 const uint8_t* __restrict__ a,
+                                                                 float* __restrict__ c, int T, int M, int K) {
+    using S = RawStep<KB>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int nb = K >> 5;
+    const uint32_t row_bytes = (uint32_t)nb * 34u;
+    const int t0 = blockIdx.y * kTT, j0 = blockIdx.x * kTM;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wt = wave >> 1, wm = wave & 1;
+    const auto ar = make_rsrc(a, row_bytes * (uint32_t)T);
+    const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
+
+    // piece q = (staged row q / kPieces, 16-byte piece q % kPieces); A rows first
+    uint32_t goff[S::kPerThread], loff[S::kPerThread];
+    bool is_a[S::kPerThread], live[S::kPerThread];
+#pragma unroll
+    for (int i = 0; i < S::kPerThread; ++i) {
+        const int q = (int)threadIdx.x + kThreadsG * i;
+        live[i] = q < S::kTotal;
+        const int qq = live[i] ? q : 0;
+        const int r = qq / S::kPieces, k = qq - r * S::kPieces;
+        is_a[i] = r < kTT;
+        const int grow = is_a[i] ? t0 + r : j0 + (r - kTT);
+        goff[i] = (uint32_t)grow * row_bytes + 16u * (uint32_t)k;
+        loff[i] = (uint32_t)(r * S::kPitch + 16 * k);
+    }
+    uint4 pre[S::kPerThread];
+    auto fetch = [&](int kb0) {
+#pragma unroll
+        for (int i = 0; i < S::kPerThread; ++i)
+            if (live[i]) pre[i] = buf_load_b128(is_a[i] ? ar : wr, goff[i] + (uint32_t)kb0 * 34u);
+    };
+    auto park = [&](uint8_t* stage) {
+#pragma unroll
+        for (int i = 0; i < S::kPerThread; ++i)
+            if (live[i]) {
+                uint32_t* d = reinterpret_cast<uint32_t*>(stage + loff[i]);  // 4-byte aligned
+                d[0] = pre[i].x;
+                d[1] = pre[i].y;
+                d[2] = pre[i].z;
+                d[3] = pre[i].w;
+            }
+    };
+
+    const int m = lane & 31, g = lane >> 5;
+    v16f acc[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[nt][i] = 0.f;
+
+    const int nsteps = nb / KB;
+    fetch(0);
+    for (int s = 0; s < nsteps; ++s) {
+        uint8_t* stage = lds + (s & 1) * S::kBytes;
+        park(stage);
+        __syncthreads();
+        if (s + 1 < nsteps) fetch((s + 1) * KB);
+        const uint8_t* arow = stage + (32 * wt + m) * S::kPitch;
+        const uint8_t* wrow0 = stage + (kTT + 64 * wm + m) * S::kPitch;
+        const uint8_t* wrow1 = wrow0 + 32 * S::kPitch;
+        // block BLK (0 or 1) of the dword-aligned pair at byte 68 bp
+        auto block = [&](auto blk_c, int bp) {
+            constexpr int BLK = decltype(blk_c)::value;
+            const uint8_t* ar_ = arow + 68 * bp;
+            const uint8_t* w0_ = wrow0 + 68 * bp;
+            const uint8_t* w1_ = wrow1 + 68 * bp;
+            const v4i av = raw_qs<BLK>(ar_, g);
+            const v4h da = raw_scale<BLK>(ar_);
+            const v4i bv0 = raw_qs<BLK>(w0_, g);
+            const v4h dw0 = raw_scale<BLK>(w0_);
+            const v4i bv1 = raw_qs<BLK>(w1_, g);
+            const v4h dw1 = raw_scale<BLK>(w1_);
+            const v16i zi = {};
+            const v16f zf = {};
+            const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv0, zi, 0, 0, 0);
+            const v16f s0 = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw0, zf, 0, 0, 0);  // 2 d_a d_w
+            const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv1, zi, 0, 0, 0);
+            const v16f s1 = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw1, zf, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[0][i] = fmaf((float)d0[i], s0[i], acc[0][i]);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[1][i] = fmaf((float)d1[i], s1[i], acc[1][i]);
+        };
+#pragma unroll 1
+        for (int bp = 0; bp < KB / 2; ++bp) {
+            block(std::integral_constant<int, 0>{}, bp);
+            block(std::integral_constant<int, 1>{}, bp);
+        }
+    }
+
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+        const int col = j0 + 64 * wm + 32 * nt + m;
+        if (col >= M) continue;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = t0 + 32 * wt + 8 * (i / 4) + 4 * g + i % 4;
+            if (row < T) c[(size_t)row * M + col] = 0.5f * acc[nt][i];  // the scales entered doubled
+        }
+    }
+}
+
 }  // namespace
 
 int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t M, int64_t K, hipStream_t st) {
@@ -173,11 +360,22 @@ int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t 
     if ((uintptr_t)w % 4 || (uintptr_t)a % 4) return fail(kInvalidArgument, "gemm: blocks must be 4-byte aligned");
     const dim3 grid((unsigned)((M + kTM - 1) / kTM), (unsigned)((T + kTT - 1) / kTT));
     if (grid.y > 65535) return fail(kInvalidArgument, "gemm: T too large");
-    const size_t lds = 2 * (size_t)kStageBytes;
-    const int rc = dynamic_lds((const void*)gemm_q8_0_kernel, lds);
-    if (rc) return rc;
-    hipLaunchKernelGGL(gemm_q8_0_kernel, grid, dim3(kThreadsG), lds, st, static_cast<const uint8_t*>(w),
-                       static_cast<const uint8_t*>(a), c, (int)T, (int)M, (int)K);
+    if ((K / 32) % 2 == 0) {
+        constexpr int kKB = 2;
+        const size_t lds = 2 * (size_t)RawStep<kKB>::kBytes;
+        const int rc = dynamic_lds((const void*)gemm_q8_0_coalesced<kKB>, lds);
+        if (rc) return rc;
+        hipLaunchKernelGGL((gemm_q8_0_coalesced<kKB>), grid, dim3(kThreadsG), lds, st, static_cast<const uint8_t*>(w),
+                           static_cast<const uint8_t*>(a), c, (int)T, (int)M, (int)K);
+    } else {
+        // any K % 32 == 0: blocks staged one by one, qs realigned on the way into LDS
+        constexpr int kKB = 4;
+        const size_t lds = 2 * (size_t)Step<kKB>::kBytes;
+        const int rc = dynamic_lds((const void*)gemm_q8_0_kernel<kKB, false>, lds);
+        if (rc) return rc;
+        hipLaunchKernelGGL((gemm_q8_0_kernel<kKB, false>), grid, dim3(kThreadsG), lds, st,
+                           static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(a), c, (int)T, (int)M, (int)K);
+    }
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

@@ -87,6 +87,23 @@ def test_gemm_one_hot_activation_picks_dequantized_weights(hip, oracle):
         np.testing.assert_allclose(c[t], wd[:, (37 * t) % K] * np.float32(127) * d_a, rtol=1e-6)
 
 
+def test_gemm_subnormal_and_extreme_scales(hip, oracle):
+    """fp16 scales that are subnormal (below 2^-14) or near the fp16 maximum:
+    the scale product must stay exact, as the oracle's fp32 product is."""
+    T, M, K = 64, 128, 512
+    w_blocks, a_blocks = _problem(13, T, M, K)
+    rng = np.random.default_rng(14)
+    sub = np.array([2.0 ** -24, 3 * 2.0 ** -20, 2.0 ** -15, 6.0e-5], np.float16).view(np.uint8).reshape(-1, 2)
+    big = np.array([60000.0, 1024.5, 0.5], np.float16).view(np.uint8).reshape(-1, 2)
+    for blocks, pool in ((w_blocks, sub), (a_blocks, np.concatenate([sub, big]))):
+        pick = rng.integers(0, len(pool), blocks.shape[:2])
+        mask = rng.random(blocks.shape[:2]) < 0.3
+        blocks[mask, 0:2] = pool[pick[mask]]
+    c = _gemm(hip, w_blocks, a_blocks)
+    c_ref = oracle.gemm_q8_0(w_blocks, a_blocks, NT)
+    np.testing.assert_array_equal(c, c_ref)
+
+
 def test_gemm_zero_scales_give_zero(hip):
     w_blocks, a_blocks = _problem(12, 64, 128, 256)
     w_blocks[..., 0:2] = 0
