@@ -46,6 +46,13 @@ __device__ __forceinline__ uint4 buf_load_b128(__amdgpu_buffer_rsrc_t r, uint32_
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// Streaming variant: the nontemporal hint keeps read-once weights from
+// displacing reused lines in the caches.
+__device__ __forceinline__ uint4 buf_load_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ uint2 buf_load_b64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
     return make_uint2(v[0], v[1]);

@@ -1,0 +1,256 @@
+"""Single-token decode of a Llama-shaped model with every tensor resident in HBM.
+
+GPU counterpart of ``AsmEngineForward`` (src/runtime/generate.py:208-326).
+The reference sequences one token as embed row -> per layer [RMSNorm, q/k/v
+matvecs, RoPE per head, KV-cache write, per-head QK^T -> softmax -> PV, o
+matvec + residual, RMSNorm, gate/up matvecs, SiLU*up, down matvec + residual]
+-> final RMSNorm -> lm-head (generate.py:261-326), with numpy arrays between
+native calls.  Here the same sequence is a fixed list of launches on one
+stream, so it can be captured once into a HIP graph and replayed per token:
+
+  * q, k and v weights are stacked into one [q; k; v] Q4_0 matrix and gate/up
+    into one [gate; up] matrix (rows are independent, so y is the same as
+    three or two separate matvecs); the RMSNorms are fused into the read of x
+    by the matvec that follows them, SiLU*up into the down matvec's read, and
+    both residual adds into the o and down matvecs (accumulate);
+  * the token id and the position live in device ints: the embedding kernel
+    reads the token, RoPE / the KV write / attention read the position, and
+    the argmax kernel writes the next token and advances the position, so a
+    replayed graph walks the sequence without host involvement;
+  * the KV cache is fp16, head-major [n_kv_heads][max_ctx][head_dim] per layer
+    (the reference keeps fp32 [128][heads][head_dim], generate.py:252-253).
+
+All weights are Q4_0 GGUF blocks, including the token embedding and the
+lm-head (generate.py:182-184 loads both through get_tensor).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import native
+from .device import DeviceBuffer, Graph, Stream
+from .gguf import q4_0_nbytes
+from .native import check
+
+
+@dataclass(frozen=True)
+class LlamaShape:
+    """Model hyper-parameters (generate.py:123-141 reads the same fields from GGUF metadata)."""
+
+    dim: int = 4096
+    n_layers: int = 32
+    n_heads: int = 32
+    n_kv_heads: int = 32
+    hidden_dim: int = 11008
+    vocab: int = 32000
+    eps: float = 1e-6
+    theta: float = 10000.0
+
+    @property
+    def head_dim(self) -> int:
+        return self.dim // self.n_heads
+
+    @property
+    def kv_dim(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+    @property
+    def qkv_rows(self) -> int:
+        return self.dim + 2 * self.kv_dim
+
+    def layer_weight_bytes(self) -> int:
+        d, h = self.dim, self.hidden_dim
+        return (q4_0_nbytes(self.qkv_rows, d) + q4_0_nbytes(d, d) + q4_0_nbytes(2 * h, d) +
+                q4_0_nbytes(d, h))
+
+    def weight_bytes(self) -> int:
+        """Q4_0 bytes one token step reads: every layer plus the lm-head
+        (the embedding table contributes one row)."""
+        return self.n_layers * self.layer_weight_bytes() + q4_0_nbytes(self.vocab, self.dim)
+
+    def kv_bytes_per_position(self) -> int:
+        return self.n_layers * 2 * self.kv_dim * 2
+
+
+LLAMA_7B = LlamaShape()
+
+
+class _Layer:
+    def __init__(self, s: LlamaShape, max_ctx: int):
+        d, h = s.dim, s.hidden_dim
+        self.attn_norm = DeviceBuffer(4 * d)
+        self.ffn_norm = DeviceBuffer(4 * d)
+        self.wqkv = DeviceBuffer(q4_0_nbytes(s.qkv_rows, d))
+        self.wo = DeviceBuffer(q4_0_nbytes(d, d))
+        self.wgu = DeviceBuffer(q4_0_nbytes(2 * h, d))
+        self.wdown = DeviceBuffer(q4_0_nbytes(d, h))
+        self.k_cache = DeviceBuffer(2 * s.n_kv_heads * max_ctx * s.head_dim)
+        self.v_cache = DeviceBuffer(2 * s.n_kv_heads * max_ctx * s.head_dim)
+
+
+class DecodeEngine:
+    """Greedy single-token decode on one GPU (AsmEngineForward, generate.py:208-326).
+
+    ``init_random`` fills the model the way the synthetic benchmark model is
+    specified: linear weights N(0, stddev^2) quantized to Q4_0 on the GPU, norm
+    weights 1, KV cache N(0, 1) in fp16.  ``load_*`` methods take host GGUF
+    blocks instead.
+    """
+
+    def __init__(self, shape: LlamaShape = LLAMA_7B, max_ctx: int = 2176, stream: Stream | None = None):
+        s = shape
+        if s.dim % s.n_heads or s.n_heads % s.n_kv_heads:
+            raise ValueError("dim must split into heads, and heads into kv groups")
+        if s.head_dim not in (64, 128):
+            raise ValueError("head_dim must be 64 or 128")
+        if s.dim % 32 or s.hidden_dim % 32:
+            raise ValueError("dim and hidden_dim must be multiples of 32 (Q4_0 blocks)")
+        self.shape = s
+        self.max_ctx = int(max_ctx)
+        self.stream = stream or Stream()
+        self.lib = native.lib()
+        self.layers = [_Layer(s, self.max_ctx) for _ in range(s.n_layers)]
+        self.embed = DeviceBuffer(q4_0_nbytes(s.vocab, s.dim))
+        self.final_norm = DeviceBuffer(4 * s.dim)
+        self.output = DeviceBuffer(q4_0_nbytes(s.vocab, s.dim))
+        # activations
+        self.x = DeviceBuffer(4 * s.dim)
+        self.qkv = DeviceBuffer(4 * s.qkv_rows)
+        self.attn = DeviceBuffer(4 * s.dim)
+        self.gu = DeviceBuffer(4 * 2 * s.hidden_dim)
+        self.logits = DeviceBuffer(4 * s.vocab)
+        ws = self.lib.asmhip_attention_decode_workspace(s.n_heads, s.head_dim, self.max_ctx)
+        self.workspace = DeviceBuffer(4 * max(int(ws), 1))
+        self.token = DeviceBuffer(4)
+        self.pos = DeviceBuffer(4)
+        self._graph: Graph | None = None
+
+    # ---- model data ---------------------------------------------------------------
+
+    def init_random(self, seed: int = 42, stddev: float = 0.02, kv_stddev: float = 1.0) -> None:
+        s, L, st = self.shape, self.lib, self.stream.handle
+        d, h = s.dim, s.hidden_dim
+
+        def blocks(buf, rows, K, tag):
+            check(L.asmhip_random_blocks(native.Q4_0, buf.ptr, rows, K, seed * 1000003 + tag, stddev, st),
+                  "random weights")
+
+        for i, ly in enumerate(self.layers):
+            base = 16 * (i + 1)
+            blocks(ly.wqkv, s.qkv_rows, d, base + 0)
+            blocks(ly.wo, d, d, base + 1)
+            blocks(ly.wgu, 2 * h, d, base + 2)
+            blocks(ly.wdown, d, h, base + 3)
+            for buf in (ly.attn_norm, ly.ffn_norm):
+                check(L.asmhip_fill_f32(buf.ptr, d, 1.0, st), "norm weights")
+            n_kv = s.n_kv_heads * self.max_ctx * s.head_dim
+            check(L.asmhip_random_f16(ly.k_cache.ptr, n_kv, seed * 1000003 + base + 4, kv_stddev, st), "kv")
+            check(L.asmhip_random_f16(ly.v_cache.ptr, n_kv, seed * 1000003 + base + 5, kv_stddev, st), "kv")
+        blocks(self.embed, s.vocab, d, 1)
+        blocks(self.output, s.vocab, d, 2)
+        check(L.asmhip_fill_f32(self.final_norm.ptr, d, 1.0, st), "norm weights")
+        self.stream.synchronize()
+
+    def load_layer(self, i: int, *, attn_norm, wq, wk, wv, wo, ffn_norm, w_gate, w_up, w_down) -> None:
+        """Host GGUF Q4_0 blocks ([rows][K/32][18] uint8) and fp32 norm weights
+        of layer i (the tensors generate.py:186-205 collects per layer)."""
+        ly = self.layers[i]
+        ly.attn_norm.upload(np.asarray(attn_norm, np.float32))
+        ly.ffn_norm.upload(np.asarray(ffn_norm, np.float32))
+        ly.wqkv.upload(np.concatenate([wq, wk, wv], axis=0))
+        ly.wo.upload(wo)
+        ly.wgu.upload(np.concatenate([w_gate, w_up], axis=0))
+        ly.wdown.upload(w_down)
+
+    def load_globals(self, *, embed, final_norm, output) -> None:
+        self.embed.upload(embed)
+        self.final_norm.upload(np.asarray(final_norm, np.float32))
+        self.output.upload(output)
+
+    def load_kv(self, i: int, k_cache: np.ndarray, v_cache: np.ndarray) -> None:
+        """fp16 caches of layer i as [n_kv_heads][max_ctx][head_dim] (uint16 bits or float16)."""
+        s = self.shape
+        want = (s.n_kv_heads, self.max_ctx, s.head_dim)
+        for buf, arr in ((self.layers[i].k_cache, k_cache), (self.layers[i].v_cache, v_cache)):
+            a = np.ascontiguousarray(arr).view(np.uint16)
+            if a.shape != want:
+                raise ValueError(f"cache shape {a.shape} != {want}")
+            buf.upload(a)
+
+    # ---- one token ------------------------------------------------------------------
+
+    def enqueue_step(self) -> None:
+        """Launches one token step on the engine's stream: logits for the token
+        in ``token`` at position ``pos``, then token <- argmax, pos += 1."""
+        s, L, st = self.shape, self.lib, self.stream.handle
+        d, h, hd = s.dim, s.hidden_dim, s.head_dim
+        eps = ctypes.c_float(s.eps)
+        Q4, RMS, SWI, NONE = native.Q4_0, native.PRE_RMSNORM, native.PRE_SWIGLU, native.PRE_NONE
+
+        def mv(w, x, y, M, K, pre, arg, acc, what):
+            check(L.asmhip_matmul_fused(Q4, w.ptr, x.ptr, y, M, K, pre, arg, eps, acc, st), what)
+
+        check(L.asmhip_embed_q4_0(self.embed.ptr, self.token.ptr, self.x.ptr, s.vocab, d, st), "embed")
+        for ly in self.layers:
+            mv(ly.wqkv, self.x, self.qkv.ptr, s.qkv_rows, d, RMS, ly.attn_norm.ptr, 0, "qkv matvec")
+            check(L.asmhip_rope_kv_write(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr, s.n_heads, s.n_kv_heads, hd,
+                                         self.pos.ptr, self.max_ctx, ctypes.c_float(s.theta), st), "rope/kv write")
+            check(L.asmhip_attention_decode(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr, self.workspace.ptr,
+                                            self.attn.ptr, s.n_heads, s.n_kv_heads, hd, self.pos.ptr, self.max_ctx,
+                                            st), "attention")
+            mv(ly.wo, self.attn, self.x.ptr, d, d, NONE, None, 1, "o matvec")
+            mv(ly.wgu, self.x, self.gu.ptr, 2 * h, d, RMS, ly.ffn_norm.ptr, 0, "gate/up matvec")
+            mv(ly.wdown, self.gu, self.x.ptr, d, h, SWI, self.gu.ptr + 4 * h, 1, "down matvec")
+        mv(self.output, self.x, self.logits.ptr, s.vocab, d, RMS, self.final_norm.ptr, 0, "lm-head matvec")
+        check(L.asmhip_argmax(self.logits.ptr, s.vocab, self.token.ptr, self.pos.ptr, st), "argmax")
+
+    def set_position(self, token_id: int, pos: int) -> None:
+        if not 0 <= pos < self.max_ctx:
+            raise ValueError(f"position {pos} outside the cache (max_ctx {self.max_ctx})")
+        if not 0 <= token_id < self.shape.vocab:
+            raise ValueError(f"token {token_id} outside the vocabulary")
+        self.token.upload(np.array([token_id], np.int32))
+        self.pos.upload(np.array([pos], np.int32))
+
+    def forward_token(self, token_id: int, pos: int) -> np.ndarray:
+        """Logits of ``token_id`` at ``pos`` (generate.py:261-326); the KV cache
+        row ``pos`` of every layer is written as a side effect."""
+        self.set_position(token_id, pos)
+        self.enqueue_step()
+        self.stream.synchronize()
+        return self.logits.download(np.float32, (self.shape.vocab,))
+
+    def capture(self) -> Graph:
+        """One token step as a HIP graph (captured once, replayed per token)."""
+        if self._graph is None:
+            self._graph = Graph.capture(self.stream, self.enqueue_step)
+        return self._graph
+
+    def generate(self, token_id: int, pos: int, n_steps: int, use_graph: bool = True) -> list[int]:
+        """Greedy decode of n_steps tokens starting from token_id at pos
+        (the loop of generate.py:411-430, argmax on the GPU)."""
+        if pos + n_steps > self.max_ctx:
+            raise ValueError("decode would run past the KV cache")
+        self.set_position(token_id, pos)
+        out = []
+        graph = self.capture() if use_graph else None
+        for _ in range(n_steps):
+            if graph is not None:
+                graph.launch(self.stream)
+            else:
+                self.enqueue_step()
+            self.stream.synchronize()
+            out.append(int(self.token.download(np.int32, (1,))[0]))
+        return out
+
+    def read_position(self) -> int:
+        return int(self.pos.download(np.int32, (1,))[0])
+
+    def close(self) -> None:
+        if self._graph is not None:
+            self._graph.close()
+            self._graph = None

@@ -188,6 +188,172 @@ def bench_cpu_baseline(seconds: float, copies: int = 4) -> dict:
     }
 
 
+def _rotating_blocks(qtype: int, M: int, K: int, copies: int, seed: int):
+    """`copies` device copies of one synthetic GGUF matrix, generated on the GPU."""
+    from asmllm_amd import gguf, native
+    from asmllm_amd.device import DeviceBuffer
+
+    lib = native.lib()
+    nbytes = gguf.q4_0_nbytes(M, K) if qtype == native.Q4_0 else gguf.q8_0_nbytes(M, K)
+    first = DeviceBuffer(nbytes)
+    native.check(lib.asmhip_random_blocks(qtype, first.ptr, M, K, seed, 0.02, None), "random blocks")
+    bufs = [first]
+    for _ in range(copies - 1):
+        b = DeviceBuffer(nbytes)
+        b.copy_from(first)
+        bufs.append(b)
+    return bufs, nbytes
+
+
+def time_launches(enqueue, copies: int, reps: int) -> float:
+    """Mean GPU microseconds of one launch: `enqueue(i)` for i < copies captured
+    into one graph, replayed `reps` times between HIP events."""
+    from asmllm_amd.device import Event, Graph, Stream, synchronize
+
+    stream = Stream()
+    graph = Graph.capture(stream, lambda: [enqueue(i, stream.handle) for i in range(copies)])
+    for _ in range(2):
+        graph.launch(stream)
+    synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(stream)
+    for _ in range(reps):
+        graph.launch(stream)
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) * 1e3 / (reps * copies)
+    graph.close()
+    return us
+
+
+# Matvec shapes of the benchmark configurations: the Q8_0 4096x4096 matvec, the
+# Llama-7B decode set and the Llama-3-8B layer sweep (GQA: k/v 1024 rows).
+MATVEC_TABLE = [
+    ("q8_0 4096x4096", "q8", 4096, 4096),
+    ("q4_0 4096x4096", "q4", 4096, 4096),
+    ("q4_0 11008x4096", "q4", 11008, 4096),
+    ("q4_0 4096x11008", "q4", 4096, 11008),
+    ("llama3 q 4096x4096", "q4", 4096, 4096),
+    ("llama3 k 1024x4096", "q4", 1024, 4096),
+    ("llama3 v 1024x4096", "q4", 1024, 4096),
+    ("llama3 o 4096x4096", "q4", 4096, 4096),
+    ("llama3 gate 14336x4096", "q4", 14336, 4096),
+    ("llama3 up 14336x4096", "q4", 14336, 4096),
+    ("llama3 down 4096x14336", "q4", 4096, 14336),
+]
+
+
+def bench_matvec_table(min_rotated_bytes: int = 600_000_000) -> list[dict]:
+    """GB/s of every configured matvec shape, weights rotating over enough
+    copies (>= 600 MB) that HBM serves them."""
+    from asmllm_amd import native
+    from asmllm_amd.device import DeviceBuffer
+
+    lib = native.lib()
+    rows = []
+    for name, qt, M, K in MATVEC_TABLE:
+        qtype = native.Q4_0 if qt == "q4" else native.Q8_0
+        blk = 18 if qt == "q4" else 34
+        copies = max(8, -(-min_rotated_bytes // (M * (K // 32) * blk)))
+        bufs, nbytes = _rotating_blocks(qtype, M, K, copies, seed=M * 7 + K)
+        dx, dy = DeviceBuffer(4 * K), DeviceBuffer(4 * M)
+        native.check(lib.asmhip_fill_f32(dx.ptr, K, 0.5, None), "fill")
+        fn = lib.asmhip_matmul_q4_0 if qt == "q4" else lib.asmhip_matmul_q8_0
+
+        def enqueue(i, st, fn=fn, bufs=bufs, dx=dx, dy=dy, M=M, K=K):
+            native.check(fn(bufs[i % len(bufs)].ptr, dx.ptr, dy.ptr, M, K, st), name)
+
+        us = time_launches(enqueue, copies, reps=max(4, 4000 // copies))
+        algo = M * (K // 32) * blk + 4 * K + 4 * M
+        rows.append({"op": name, "us": round(us, 3), "GBps": round(algo / us / 1e3, 1),
+                     "frac": round(algo / us / 1e3 / HBM_PEAK_GBPS, 4), "bytes": algo})
+        for b in bufs:
+            b.close()
+        log(f"{name}: {us:.3f} us, {algo / us / 1e3:.0f} GB/s")
+    layer = [r for r in rows if r["op"].startswith("llama3")]
+    us = sum(r["us"] for r in layer)
+    nbytes = sum(r["bytes"] for r in layer)
+    rows.append({"op": "llama3 layer (7 matvecs)", "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
+                 "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4), "bytes": nbytes})
+    return rows
+
+
+INT8_MFMA_PEAK_TOPS = 5000.0
+
+
+def bench_gemm(T: int = 512, M: int = 11008, K: int = 4096, copies: int = 12) -> dict:
+    """Q8_0 x Q8_0 prefill GEMM: activations 512x4096 fp32 quantized per row on
+    the GPU, weights 11008x4096 Q8_0; ops = 2*T*M*K."""
+    from asmllm_amd import gguf, native
+    from asmllm_amd.device import DeviceBuffer
+
+    lib = native.lib()
+    wbufs, _ = _rotating_blocks(native.Q8_0, M, K, copies, seed=99)
+    da = DeviceBuffer(4 * T * K)
+    native.check(lib.asmhip_fill_f32(da.ptr, T * K, 0.25, None), "fill")
+    dq = DeviceBuffer(gguf.q8_0_nbytes(T, K))
+    native.check(lib.asmhip_random_blocks(native.Q8_0, dq.ptr, T, K, 5, 1.0, None), "random activations")
+    dc = DeviceBuffer(4 * T * M)
+
+    def gemm(i, st):
+        native.check(lib.asmhip_gemm_q8_0(wbufs[i % copies].ptr, dq.ptr, dc.ptr, T, M, K, st), "gemm")
+
+    def quant(i, st):
+        native.check(lib.asmhip_quantize(native.Q8_0, da.ptr, dq.ptr, T, K, st), "quantize")
+
+    us = time_launches(gemm, copies, reps=20)
+    us_q = time_launches(quant, copies, reps=20)
+    ops = 2 * T * M * K
+    nbytes = gguf.q8_0_nbytes(M, K) + gguf.q8_0_nbytes(T, K) + 4 * T * M
+    log(f"GEMM {T}x{M}x{K}: {us:.2f} us, {ops / us / 1e6:.0f} TOP/s")
+    return {"workload": f"Q8_0 GEMM C[{T}][{M}] = A_q8[{T}][{K}] . W_q8[{M}][{K}]^T", "us": round(us, 3),
+            "TOPs": round(ops / us / 1e6, 1), "frac_int8_mfma_peak": round(ops / us / 1e6 / INT8_MFMA_PEAK_TOPS, 4),
+            "GBps": round(nbytes / us / 1e3, 1), "activation_quantize_us": round(us_q, 3), "ops": ops,
+            "bytes": nbytes}
+
+
+def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4) -> dict:
+    """Greedy single-token decode of the 32-layer 7B-shape Q4_0 model, fp16 KV
+    cache prefilled to `context`: `steps` tokens from position `context`,
+    each one replay of the captured token-step graph (token and position stay
+    on the GPU between steps)."""
+    from asmllm_amd.device import Event, synchronize
+    from asmllm_amd.engine import LLAMA_7B, DecodeEngine
+
+    s = LLAMA_7B
+    eng = DecodeEngine(s, max_ctx=context + steps)
+    eng.init_random(seed=42)
+    graph = eng.capture()
+    eng.set_position(1, context)
+    for _ in range(warmup):
+        graph.launch(eng.stream)
+    eng.stream.synchronize()
+    eng.set_position(1, context)
+    synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(eng.stream)
+    for _ in range(steps):
+        graph.launch(eng.stream)
+    e1.record(eng.stream)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1)
+    end_pos = eng.read_position()
+    if end_pos != context + steps:
+        raise SystemExit(f"decode: position {end_pos} after {steps} steps from {context}")
+    # HBM bytes per token: all Q4_0 weights + one embedding row + the KV cache
+    # read (positions 0..pos, k and v, every layer) + the new k/v row written
+    kv_read = sum((p + 1) for p in range(context, context + steps)) / steps * s.kv_bytes_per_position()
+    per_token = s.weight_bytes() + (s.dim // 32) * 18 + kv_read + s.kv_bytes_per_position()
+    tok_s = steps / (ms / 1e3)
+    eng.close()
+    log(f"decode: {tok_s:.1f} tokens/s ({ms / steps:.3f} ms/token)")
+    return {"workload": f"7B-shape Q4_0 Llama greedy decode, {s.n_layers} layers, d {s.dim}, {s.n_heads}x"
+                        f"{s.head_dim} heads, FFN {s.hidden_dim}, vocab {s.vocab}, fp16 KV prefilled to {context}",
+            "tokens_per_s": round(tok_s, 2), "ms_per_token": round(ms / steps, 4), "steps": steps,
+            "context": context, "bytes_per_token": int(per_token),
+            "GBps": round(per_token * tok_s / 1e9, 1), "frac": round(per_token * tok_s / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def profile_pass(copies: int, launches: int = 64) -> None:
     """A short fixed workload for hardware-counter runs: `launches` matvecs
     over rotating weight copies, then the calibration kernel (exact Q4_0
@@ -290,6 +456,8 @@ def main() -> None:
     ap.add_argument("--profile-pass", action="store_true",
                     help="run only a short fixed workload for hardware-counter collection")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--no-extra", action="store_true", help="skip the shape table, GEMM and decode legs")
+    ap.add_argument("--only", choices=["decode", "gemm", "table"], help="run one extra leg and print its JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build has no multi-GPU path)",
@@ -302,10 +470,20 @@ def main() -> None:
 
     from asmllm_amd.device import device_info
 
+    if args.only:
+        leg = {"decode": bench_decode, "gemm": bench_gemm, "table": bench_matvec_table}[args.only]
+        print(json.dumps({args.only: leg()}), flush=True)
+        return
+
     info = device_info()
     log(f"device {info['arch']} with {info['compute_units']} CUs")
     mv = bench_matvec(args.steps, args.warmup, args.copies)
     achieved = mv["bytes_per_step"] / (mv["kernel_us_mean"] * 1e-6) / 1e9
+    extra = {}
+    if not args.no_extra:
+        extra["decode"] = bench_decode()
+        extra["gemm"] = bench_gemm()
+        extra["matvec_table"] = bench_matvec_table()
     cpu = None if args.no_cpu else bench_cpu_baseline(args.cpu_seconds)
     traffic = None if args.no_traffic else measure_traffic()
 
@@ -345,6 +523,7 @@ def main() -> None:
         "cpu_baseline": cpu,
         "parity_max_err_over_l1": mv["parity_max_err_over_l1"],
     }
+    result.update(extra)
     print(json.dumps(result), flush=True)
 
 

@@ -1,0 +1,77 @@
+"""CPU single-token decode, composed from the oracle's decode ops (TEST INFRASTRUCTURE ONLY).
+
+Restates ``AsmEngineForward.forward_token`` (src/runtime/generate.py:261-326)
+step for step, with the two storage choices of the GPU engine made explicit:
+the KV cache holds fp16 values (k after RoPE and v, rounded to nearest even
+when written), head-major [n_kv_heads][max_ctx][head_dim]; and heads may be
+grouped (n_heads / n_kv_heads query heads per kv head; the reference has
+n_heads == n_kv_heads).  Every arithmetic step calls an oracle function that
+tests/test_oracle.py pins on its own:
+
+  * matvecs: oracle_matmul_q4_0_gguf (matmul_q4_avx2.asm:110-178 over GGUF
+    blocks, scale widened from fp16 as generate.py:91-106 does);
+  * rmsnorm (rmsnorm_avx2.asm:63-151), rope (rope_avx2.asm:52-146),
+    silu_hadamard (swiglu_avx2.asm:45-81);
+  * attention over the fp16 cache: oracle_attention_decode_f16, the
+    reference's per-head QK^T/sqrt(hd) -> softmax -> PV (generate.py:291-296).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import native as o
+
+
+class DecodeRef:
+    """Host copy of a decode model: GGUF Q4_0 blocks ([rows][K/32][18] uint8),
+    fp32 norm weights, fp16 caches [n_kv][max_ctx][hd] as uint16 bits."""
+
+    def __init__(self, *, dim, n_heads, n_kv_heads, hidden_dim, vocab, eps, theta, embed, final_norm, output,
+                 layers, k_caches, v_caches, nt: int = 1):
+        self.dim, self.n_heads, self.n_kv_heads = dim, n_heads, n_kv_heads
+        self.hidden_dim, self.vocab, self.eps, self.theta = hidden_dim, vocab, eps, theta
+        self.hd = dim // n_heads
+        self.embed, self.final_norm, self.output = embed, final_norm, output
+        self.layers = layers            # dicts: attn_norm wq wk wv wo ffn_norm w_gate w_up w_down
+        self.k_caches = [np.array(k, np.uint16) for k in k_caches]
+        self.v_caches = [np.array(v, np.uint16) for v in v_caches]
+        self.nt = nt
+
+    def _mv(self, blocks, x):
+        return o.matmul_q4_0_gguf(blocks, x, self.nt)
+
+    def _rope_heads(self, v, n):
+        """RoPE on n heads of v (rope_avx2.asm rotates one q head and one k head per call)."""
+        out = v.reshape(n, self.hd).copy()
+        for h in range(n):
+            out[h], _ = o.rope(out[h], out[h], self.hd, self._pos, self.theta)
+        return out.reshape(-1)
+
+    def forward_token(self, token_id: int, pos: int) -> np.ndarray:
+        """Logits of token_id at pos; writes cache row pos (generate.py:261-326)."""
+        self._pos = pos
+        hd, nh, nkv = self.hd, self.n_heads, self.n_kv_heads
+        x = o.dequantize_q4_0(self.embed[token_id:token_id + 1])[0].copy()        # :262
+        for li, ly in enumerate(self.layers):
+            xn = o.rmsnorm(x, ly["attn_norm"], self.eps)                          # :268-272
+            q = self._mv(ly["wq"], xn)                                            # :278-280
+            k = self._mv(ly["wk"], xn)
+            v = self._mv(ly["wv"], xn)
+            q = self._rope_heads(q, nh)                                           # :282-285
+            k = self._rope_heads(k, nkv)
+            kc, vc = self.k_caches[li], self.v_caches[li]                         # :289-290
+            kc[:, pos, :] = k.reshape(nkv, hd).astype(np.float16).view(np.uint16)
+            vc[:, pos, :] = v.reshape(nkv, hd).astype(np.float16).view(np.uint16)
+            # position-major view [pos][n_kv][hd] for the oracle kernel
+            kp = np.ascontiguousarray(kc[:, :pos + 1, :].transpose(1, 0, 2))
+            vp = np.ascontiguousarray(vc[:, :pos + 1, :].transpose(1, 0, 2))
+            attn = o.attention_decode_f16(q.reshape(nh, hd), kp, vp, pos + 1, nkv, self.nt)   # :291-296
+            x = x + self._mv(ly["wo"], attn.reshape(-1))                          # :298-300
+            xn = o.rmsnorm(x, ly["ffn_norm"], self.eps)                           # :302-306
+            gate = self._mv(ly["w_gate"], xn)                                     # :308-311
+            up = self._mv(ly["w_up"], xn)
+            g = o.silu_hadamard(gate, up)                                         # :313
+            x = x + self._mv(ly["w_down"], g)                                     # :315-317
+        xn = o.rmsnorm(x, self.final_norm, self.eps)                              # :319-323
+        return self._mv(self.output, xn)                                          # :325

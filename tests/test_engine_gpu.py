@@ -1,0 +1,125 @@
+"""GPU decode engine (asmllm_amd.engine) against the oracle's composed decode step.
+
+The engine's weights and caches are read back from HBM, so both sides run on
+the same bytes.  Bar: logits within 2e-4 of the largest logit magnitude (the
+per-op fp32 tolerance, 1e-5 at test_runner.py:36, accumulated over the
+layers and the lm-head), and the greedy token equal whenever the oracle's
+top-2 margin is above that bar.  A graph replay of the step must reproduce
+the eager launches bit for bit.
+"""
+
+import numpy as np
+import pytest
+
+from asmllm_amd.engine import LLAMA_7B, DecodeEngine, LlamaShape
+from asmllm_amd.gguf import q4_0_nbytes
+
+pytestmark = pytest.mark.gpu
+LOGIT_TOL = 2e-4
+
+
+def _blocks(buf, rows, K):
+    return buf.download(np.uint8, (rows, K // 32, 18))
+
+
+def _oracle_model(eng: DecodeEngine, nt: int):
+    from oracle.decode_ref import DecodeRef
+
+    s = eng.shape
+    d, h, kv = s.dim, s.hidden_dim, s.kv_dim
+    layers, kcs, vcs = [], [], []
+    for ly in eng.layers:
+        qkv = _blocks(ly.wqkv, s.qkv_rows, d)
+        gu = _blocks(ly.wgu, 2 * h, d)
+        layers.append({
+            "attn_norm": ly.attn_norm.download(np.float32, d), "ffn_norm": ly.ffn_norm.download(np.float32, d),
+            "wq": qkv[:d], "wk": qkv[d:d + kv], "wv": qkv[d + kv:],
+            "wo": _blocks(ly.wo, d, d), "w_gate": gu[:h], "w_up": gu[h:], "w_down": _blocks(ly.wdown, d, h),
+        })
+        shape = (s.n_kv_heads, eng.max_ctx, s.head_dim)
+        kcs.append(ly.k_cache.download(np.uint16, shape))
+        vcs.append(ly.v_cache.download(np.uint16, shape))
+    return DecodeRef(dim=d, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, hidden_dim=h, vocab=s.vocab, eps=s.eps,
+                     theta=s.theta, embed=_blocks(eng.embed, s.vocab, d),
+                     final_norm=eng.final_norm.download(np.float32, d), output=_blocks(eng.output, s.vocab, d),
+                     layers=layers, k_caches=kcs, v_caches=vcs, nt=nt)
+
+
+def _check_logits(got, ref, what):
+    scale = float(np.abs(ref).max())
+    err = float(np.abs(got.astype(np.float64) - ref).max())
+    assert err <= LOGIT_TOL * scale, f"{what}: max |err| {err:.3e} > {LOGIT_TOL:.0e} x max|logit| {scale:.3e}"
+    top2 = np.sort(ref)[-2:]
+    if top2[1] - top2[0] > 2 * LOGIT_TOL * scale:
+        assert int(np.argmax(got)) == int(np.argmax(ref)), what
+    return err / scale
+
+
+SMALL = [
+    LlamaShape(dim=256, n_layers=2, n_heads=4, n_kv_heads=4, hidden_dim=512, vocab=1000),
+    LlamaShape(dim=512, n_layers=2, n_heads=4, n_kv_heads=2, hidden_dim=1408, vocab=777, eps=1e-5),
+    LlamaShape(dim=512, n_layers=3, n_heads=8, n_kv_heads=8, hidden_dim=1024, vocab=4096, theta=5e5),
+]
+
+
+@pytest.mark.parametrize("shape", SMALL, ids=["mha", "gqa", "hd64"])
+def test_decode_steps_match_oracle(shape):
+    eng = DecodeEngine(shape, max_ctx=48)
+    eng.init_random(seed=7)
+    ref = _oracle_model(eng, nt=4)
+    token, pos0 = 5, 29
+    for step in range(4):
+        pos = pos0 + step
+        got = eng.forward_token(token, pos)
+        want = ref.forward_token(token, pos)
+        rel = _check_logits(got, want, f"step {step} pos {pos}")
+        print(f"step {step}: max err / max|logit| {rel:.2e}")
+        token = int(np.argmax(want))
+    # the caches agree after the steps: k within one fp16 rounding, v likewise
+    for li, ly in enumerate(eng.layers):
+        kc = ly.k_cache.download(np.uint16, ref.k_caches[li].shape)
+        for p in range(pos0, pos0 + 4):
+            a = kc[:, p].view(np.float16).astype(np.float32)
+            b = ref.k_caches[li][:, p].view(np.float16).astype(np.float32)
+            np.testing.assert_allclose(a, b, rtol=2 ** -9, atol=1e-3)
+    eng.close()
+
+
+def test_graph_replay_matches_eager_launches():
+    shape = SMALL[0]
+    eng = DecodeEngine(shape, max_ctx=64)
+    eng.init_random(seed=3)
+    eager = eng.generate(11, 40, 6, use_graph=False)
+    logits_eager = eng.logits.download(np.float32, shape.vocab)
+    assert eng.read_position() == 46
+    graphed = eng.generate(11, 40, 6, use_graph=True)   # same start: rewrites the same cache rows
+    assert graphed == eager
+    np.testing.assert_array_equal(eng.logits.download(np.float32, shape.vocab), logits_eager)
+    assert eng.read_position() == 46
+    again = eng.generate(11, 40, 6, use_graph=True)     # replays of one captured graph
+    assert again == eager
+    eng.close()
+
+
+def test_engine_rejects_positions_outside_the_cache():
+    eng = DecodeEngine(SMALL[0], max_ctx=16)
+    with pytest.raises(ValueError):
+        eng.forward_token(1, 16)
+    with pytest.raises(ValueError):
+        eng.generate(1, 10, 7)
+    with pytest.raises(ValueError):
+        eng.forward_token(SMALL[0].vocab, 0)
+
+
+def test_7b_shape_step_at_context_2048_matches_oracle():
+    """One token of the 32-layer 7B-shape model at position 2048 (cache
+    prefilled with N(0,1) fp16), the benchmark's decode workload."""
+    eng = DecodeEngine(LLAMA_7B, max_ctx=2176)
+    eng.init_random(seed=42)
+    assert eng.layers[0].wqkv.nbytes == q4_0_nbytes(3 * 4096, 4096)
+    got = eng.forward_token(1, 2048)
+    ref = _oracle_model(eng, nt=16)
+    want = ref.forward_token(1, 2048)
+    rel = _check_logits(got, want, "7B step")
+    print(f"7B step: max err / max|logit| {rel:.2e}")
+    eng.close()

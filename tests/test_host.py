@@ -61,3 +61,14 @@ def test_reference_argtypes_mirrored():
     assert native.SIGNATURES["asm_matmul_q4"] == (None, [P, P, P, P, I64, I64])
     assert native.SIGNATURES["asm_matmul_q8"] == (None, [P, P, P, P, I64, I64])
     assert native.SIGNATURES["asm_matmul_q4_mt"] == (None, [P, P, P, P, I64, I64, ctypes.c_int])
+
+
+def test_7b_decode_byte_budget():
+    """Bytes one 7B-shape token step streams: 32 layers of Q4_0 q/k/v/o,
+    gate/up/down (113,836,032 B each) plus the 32000x4096 lm-head."""
+    from asmllm_amd.engine import LLAMA_7B
+
+    assert LLAMA_7B.layer_weight_bytes() == 113_836_032
+    assert LLAMA_7B.weight_bytes() == 3_716_481_024
+    assert LLAMA_7B.kv_bytes_per_position() == 524_288
+    assert LLAMA_7B.head_dim == 128 and LLAMA_7B.qkv_rows == 3 * 4096

@@ -258,7 +258,8 @@ def test_bad_arguments_are_rejected(hip):
 # ---- both Q4_0 GGUF kernels, selected explicitly ------------------------------------------
 
 @pytest.mark.parametrize("kernel", Q4_KERNELS, ids=["fp32", "mfma"])
-@pytest.mark.parametrize("M,K", [s[1:] for s in CONFIG_SHAPES if s[0] == "q4"] + [(16, 256), (40, 16384)])
+@pytest.mark.parametrize("M,K", [s[1:] for s in CONFIG_SHAPES if s[0] == "q4"] +
+                         [(16, 256), (40, 16384), (12288, 4096), (22016, 4096), (32000, 4096), (300, 2304)])
 def test_q4_kernels_at_config_shapes(hip, oracle, q4_kernel, kernel, M, K):
     q4_kernel(kernel)
     blocks, x = _weights(3 * M + K, M, K)
