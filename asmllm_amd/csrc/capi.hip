@@ -518,7 +518,7 @@ extern "C" int asmhip_rope_kv_write(float* qkv, void* k_cache, void* v_cache, in
 
 extern "C" int64_t asmhip_attention_decode_workspace(int n_heads, int head_dim, int max_ctx) {
     if (n_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return 0;
-    return (int64_t)n_heads * attn_decode_splits(max_ctx) * (head_dim + 2);
+    return attn_decode_workspace(n_heads, head_dim, max_ctx);
 }
 
 extern "C" int asmhip_attention_decode(const float* q, const void* k_cache, const void* v_cache, float* workspace,
@@ -527,8 +527,18 @@ extern "C" int asmhip_attention_decode(const float* q, const void* k_cache, cons
     if (!q || !k_cache || !v_cache || !workspace || !out || !pos_dev)
         return fail(kInvalidArgument, "null pointer argument");
     if (n_heads <= 0 || max_ctx <= 0) return fail(kInvalidArgument, "bad attention shape");
-    return attn_decode_launch(q, k_cache, v_cache, workspace, out, n_heads, n_kv_heads, head_dim, pos_dev, max_ctx,
-                              (hipStream_t)stream);
+    return attn_decode_launch(q, const_cast<void*>(k_cache), const_cast<void*>(v_cache), workspace, out, n_heads,
+                              n_kv_heads, head_dim, pos_dev, max_ctx, false, 0.f, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_attention_decode_rope(const float* qkv, void* k_cache, void* v_cache, float* workspace,
+                                            float* out, int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
+                                            int max_ctx, float theta, void* stream) {
+    if (!qkv || !k_cache || !v_cache || !workspace || !out || !pos_dev)
+        return fail(kInvalidArgument, "null pointer argument");
+    if (n_heads <= 0 || max_ctx <= 0 || head_dim % 2) return fail(kInvalidArgument, "bad attention shape");
+    return attn_decode_launch(qkv, k_cache, v_cache, workspace, out, n_heads, n_kv_heads, head_dim, pos_dev, max_ctx,
+                              true, theta, (hipStream_t)stream);
 }
 
 extern "C" int asmhip_embed_q4_0(const void* table, const int* token_dev, float* x, int n_vocab, int dim,

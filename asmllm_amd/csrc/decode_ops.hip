@@ -182,113 +182,192 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(const float* __restri
     }
 }
 
-// ---- decode attention over the fp16 cache, split over positions ---------------------
-// grid (n_heads, n_splits); workgroup = 4 waves; kSlots positions in flight per
-// workgroup, HD/8 lanes per position each holding 8 dimensions (16 bytes).
-// Partial result per (head, split): [m, l, acc[HD]] with acc unnormalized.
-template <int HD>
-__global__ __launch_bounds__(kBlock) void attn_decode_partial(const float* __restrict__ q,
-                                                              const __half* __restrict__ kc,
-                                                              const __half* __restrict__ vc,
-                                                              float* __restrict__ part, int n_heads, int n_kv,
-                                                              const int* __restrict__ pos_ptr, int max_ctx,
-                                                              int split_len) {
-    constexpr int kLanesPerPos = HD / 8;
-    constexpr int kSlots = kBlock / kLanesPerPos;
-    __shared__ float sc[1024];
-    __shared__ float red[kBlock / kWave];
-    __shared__ float accs[kSlots][HD + 1];
-    const int h = blockIdx.x, split = blockIdx.y;
-    const int kvh = h / (n_heads / n_kv);
-    const int n_pos = min(*pos_ptr + 1, max_ctx);
-    const int p0 = split * split_len, p1 = min(p0 + split_len, n_pos);
-    float* out = part + ((size_t)h * gridDim.y + split) * (HD + 2);
-    if (p0 >= p1) {
-        if (threadIdx.x == 0) {
-            out[0] = -INFINITY;
-            out[1] = 0.f;
-        }
-        for (int d = threadIdx.x; d < HD; d += kBlock) out[2 + d] = 0.f;
-        return;
-    }
-    const int slot = threadIdx.x / kLanesPerPos, c = threadIdx.x % kLanesPerPos;
-    const float scale = 1.0f / sqrtf((float)HD);
-    float qv[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) qv[t] = q[(size_t)h * HD + 8 * c + t] * scale;
-    const __half* kbase = kc + (size_t)kvh * max_ctx * HD;
-    const __half* vbase = vc + (size_t)kvh * max_ctx * HD;
+// ---- decode attention over the fp16 cache: one launch per layer ----------------------
+// grid (n_heads, S = ceil(max_ctx / kAttnSplitLen)); workgroup (h, s) covers
+// positions [s*kAttnSplitLen, (s+1)*kAttnSplitLen) of 0..pos.  Within a workgroup
+// a position is read by HD/8 lanes (8 dims = 16 bytes each), so a wave covers
+// 64/(HD/8) positions per row and the four waves kRowPos; every k and v load of
+// the workgroup is issued before the first score is formed.  Each lane group
+// keeps a softmax state (max m, sum l, acc[8]) over its positions; the states
+// merge across lane groups (shuffles) and waves (LDS); each workgroup writes
+// [m, l, acc[HD]] to `part`, and attn_decode_merge combines the S partials of a
+// head in split order into out = acc / l.
+//
+// ROPE = true also does what rope_kv_write does, inside the same launch: q and
+// the new k are rotated at `pos` (angles as rope_angle), the new k and v are
+// rounded to fp16 and written to the caches at `pos` (by the workgroup of the
+// first query head of the kv group), and the workgroup whose split holds `pos`
+// uses those fp16 values instead of reading the row it writes.
+template <int HD, bool ROPE>
+__global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __restrict__ qkv, __half* kc, __half* vc,
+                                                             float* __restrict__ part, int n_heads, int n_kv,
+                                                             const int* __restrict__ pos_ptr, int max_ctx,
+                                                             float theta) {
+    constexpr int kLanes = HD / 8;                        // lanes per position
+    constexpr int kGroups = kWave / kLanes;               // positions per wave and row
+    constexpr int kRowPos = kGroups * (kBlock / kWave);   // positions per workgroup and row
+    constexpr int kRows = kAttnSplitLen / kRowPos;
+    static_assert(kAttnSplitLen % kRowPos == 0, "split must hold whole rows");
+    __shared__ float cs[HD];                 // cos, sin of pair i at 2i, 2i+1
+    __shared__ float wst[kBlock / kWave][HD + 2];
 
-    // pass 1: scores
-    for (int p = p0 + slot; p < p1; p += kSlots) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(kbase + (size_t)p * HD + 8 * c);
-        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    const int h = blockIdx.x, split = blockIdx.y, S = gridDim.y;
+    const int group = n_heads / n_kv, kvh = h / group;
+    const int pos = *pos_ptr;
+    const int n_pos = (pos >= 0 && pos < max_ctx) ? pos + 1 : 0;  // an invalid position reads and writes nothing
+    const int p0 = split * kAttnSplitLen, p1 = min(p0 + kAttnSplitLen, n_pos);
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
+    const int g = lane / kLanes, c = lane % kLanes;
+    const size_t head_off = (size_t)kvh * max_ctx * HD + 8 * c;
+
+    // all k and v rows of this lane, issued up front
+    uint4 kr[kRows], vr[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const int p = p0 + r * kRowPos + w * kGroups + g;
+        const bool live = p < p1 && !(ROPE && p == pos);
+        kr[r] = live ? *reinterpret_cast<const uint4*>(kc + head_off + (size_t)p * HD) : make_uint4(0, 0, 0, 0);
+        vr[r] = live ? *reinterpret_cast<const uint4*>(vc + head_off + (size_t)p * HD) : make_uint4(0, 0, 0, 0);
+    }
+    float qv[8];
+    {
+        const float4 a = *reinterpret_cast<const float4*>(qkv + (size_t)h * HD + 8 * c);
+        const float4 b = *reinterpret_cast<const float4*>(qkv + (size_t)h * HD + 8 * c + 4);
+        qv[0] = a.x, qv[1] = a.y, qv[2] = a.z, qv[3] = a.w, qv[4] = b.x, qv[5] = b.y, qv[6] = b.z, qv[7] = b.w;
+    }
+    if constexpr (ROPE) {
+        if (threadIdx.x < HD / 2 && n_pos > 0)
+            rope_angle(threadIdx.x, HD, pos, theta, &cs[2 * threadIdx.x], &cs[2 * threadIdx.x + 1]);
+        __syncthreads();
+        if (n_pos > 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rotate(&qv[2 * i], cs[2 * (4 * c + i)], cs[2 * (4 * c + i) + 1]);
+        }
+        if (p0 <= pos && pos < p1) {
+            // the new row: rotated k and v of kv head kvh, rounded to fp16
+            const float* kn = qkv + (size_t)(n_heads + kvh) * HD + 8 * c;
+            const float* vn = qkv + (size_t)(n_heads + n_kv + kvh) * HD + 8 * c;
+            uint32_t kw[4], vw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float kk[2] = {kn[2 * i], kn[2 * i + 1]};
+                rotate(kk, cs[2 * (4 * c + i)], cs[2 * (4 * c + i) + 1]);
+                kw[i] = (uint32_t)__half_as_ushort(__float2half_rn(kk[0])) |
+                        ((uint32_t)__half_as_ushort(__float2half_rn(kk[1])) << 16);
+                vw[i] = (uint32_t)__half_as_ushort(__float2half_rn(vn[2 * i])) |
+                        ((uint32_t)__half_as_ushort(__float2half_rn(vn[2 * i + 1])) << 16);
+            }
+            const uint4 kq = make_uint4(kw[0], kw[1], kw[2], kw[3]), vq = make_uint4(vw[0], vw[1], vw[2], vw[3]);
+            const int rr = (pos - p0) / kRowPos, rem = (pos - p0) % kRowPos;
+            if (w == rem / kGroups && g == rem % kGroups) {
+#pragma unroll
+                for (int r = 0; r < kRows; ++r)
+                    if (r == rr) kr[r] = kq, vr[r] = vq;
+                if (h % group == 0) {
+                    *reinterpret_cast<uint4*>(kc + head_off + (size_t)pos * HD) = kq;
+                    *reinterpret_cast<uint4*>(vc + head_off + (size_t)pos * HD) = vq;
+                }
+            }
+        }
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) qv[t] *= scale;
+
+    // scores of this lane group's positions, then its softmax state
+    float sc[kRows];
+    float m = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const uint32_t kw[4] = {kr[r].x, kr[r].y, kr[r].z, kr[r].w};
         float d = 0.f;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            d = fmaf(qv[2 * t], half_lo(w[t]), d);
-            d = fmaf(qv[2 * t + 1], half_hi(w[t]), d);
+            d = fmaf(qv[2 * t], half_lo(kw[t]), d);
+            d = fmaf(qv[2 * t + 1], half_hi(kw[t]), d);
         }
 #pragma unroll
-        for (int o = kLanesPerPos / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, kWave);
-        if (c == 0) sc[p - p0] = d;
+        for (int o = kLanes / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, kWave);
+        const int p = p0 + r * kRowPos + w * kGroups + g;
+        sc[r] = p < p1 ? d : -INFINITY;
+        m = fmaxf(m, sc[r]);
     }
-    __syncthreads();
-    const int n = p1 - p0;
-    float m = -INFINITY;
-    for (int j = threadIdx.x; j < n; j += kBlock) m = fmaxf(m, sc[j]);
-    m = block_max<kBlock>(m, red);
-    float l = 0.f;
-    for (int j = threadIdx.x; j < n; j += kBlock) {
-        const float e = expf(sc[j] - m);
-        sc[j] = e;
-        l += e;
-    }
-    l = block_sum<kBlock>(l, red);
-    __syncthreads();
-
-    // pass 2: p . V
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p = p0 + slot; p < p1; p += kSlots) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(vbase + (size_t)p * HD + 8 * c);
-        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-        const float pr = sc[p - p0];
+    float l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (m != -INFINITY) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            acc[2 * t] = fmaf(pr, half_lo(w[t]), acc[2 * t]);
-            acc[2 * t + 1] = fmaf(pr, half_hi(w[t]), acc[2 * t + 1]);
+        for (int r = 0; r < kRows; ++r) {
+            const float e = expf(sc[r] - m);  // 0 for positions past the split
+            l += e;
+            const uint32_t vw[4] = {vr[r].x, vr[r].y, vr[r].z, vr[r].w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                acc[2 * t] = fmaf(e, half_lo(vw[t]), acc[2 * t]);
+                acc[2 * t + 1] = fmaf(e, half_hi(vw[t]), acc[2 * t + 1]);
+            }
         }
     }
+    // merge the lane groups of the wave
 #pragma unroll
-    for (int t = 0; t < 8; ++t) accs[slot][8 * c + t] = acc[t];
-    __syncthreads();
-    for (int d = threadIdx.x; d < HD; d += kBlock) {
-        float a = 0.f;
-        for (int sl = 0; sl < kSlots; ++sl) a += accs[sl][d];
-        out[2 + d] = a;
+    for (int o = kLanes; o < kWave; o <<= 1) {
+        const float m2 = __shfl_xor(m, o, kWave), l2 = __shfl_xor(l, o, kWave);
+        const float M = fmaxf(m, m2);
+        const float f1 = M == -INFINITY ? 0.f : expf(m - M), f2 = M == -INFINITY ? 0.f : expf(m2 - M);
+        l = l * f1 + l2 * f2;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] = acc[t] * f1 + __shfl_xor(acc[t], o, kWave) * f2;
+        m = M;
     }
-    if (threadIdx.x == 0) {
-        out[0] = m;
-        out[1] = l;
+    if (g == 0) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) wst[w][2 + 8 * c + t] = acc[t];
+        if (c == 0) wst[w][0] = m, wst[w][1] = l;
+    }
+    __syncthreads();
+    // merge the waves; thread t < HD owns dimension t of this workgroup's partial
+    float* mine = part + ((size_t)h * S + split) * (HD + 2);
+    if (threadIdx.x < HD) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kBlock / kWave; ++i) M = fmaxf(M, wst[i][0]);
+        float L = 0.f, a = 0.f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int i = 0; i < kBlock / kWave; ++i) {
+                const float f = expf(wst[i][0] - M);
+                L = fmaf(wst[i][1], f, L);
+                a = fmaf(wst[i][2 + threadIdx.x], f, a);
+            }
+        }
+        mine[2 + threadIdx.x] = a;
+        if (threadIdx.x == 0) mine[0] = M, mine[1] = L;
     }
 }
 
+// Merge of the S partials of head h (blockIdx.x) in split order; thread t owns
+// dimension t.  Splits past the last position hold m = -inf, l = 0.
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_decode_combine(const float* __restrict__ part, float* __restrict__ out,
-                                                          int n_splits) {
-    const int h = blockIdx.x, d = threadIdx.x;
-    const float* ph = part + (size_t)h * n_splits * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ph[(size_t)s * (HD + 2)]);
-    float L = 0.f, a = 0.f;
-    for (int s = 0; s < n_splits; ++s) {
-        const float* e = ph + (size_t)s * (HD + 2);
-        if (e[0] == -INFINITY) continue;
-        const float f = expf(e[0] - M);
-        L = fmaf(e[1], f, L);
-        a = fmaf(e[2 + d], f, a);
+__global__ __launch_bounds__(HD) void attn_decode_merge(const float* __restrict__ part, float* __restrict__ out,
+                                                        int S) {
+    __shared__ float sm[64], sl[64];
+    const int h = blockIdx.x;
+    const float* ph = part + (size_t)h * S * (HD + 2);
+    if (threadIdx.x < S) {  // S <= 64, checked at launch
+        sm[threadIdx.x] = ph[(size_t)threadIdx.x * (HD + 2)];
+        sl[threadIdx.x] = ph[(size_t)threadIdx.x * (HD + 2) + 1];
     }
-    out[(size_t)h * HD + d] = a / L;
+    __syncthreads();
+    float M = -INFINITY;
+    for (int i = 0; i < S; ++i) M = fmaxf(M, sm[i]);
+    float L = 0.f, a = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll 8
+        for (int i = 0; i < S; ++i) {
+            const float f = expf(sm[i] - M);
+            L = fmaf(sl[i], f, L);
+            a = fmaf(ph[(size_t)i * (HD + 2) + 2 + threadIdx.x], f, a);
+        }
+    }
+    out[(size_t)h * HD + threadIdx.x] = a / L;
 }
 
 // ---- embedding row of a Q4_0 table -----------------------------------------------------
@@ -407,19 +486,37 @@ int attention_launch(const float* q, const float* k, const float* v, float* y, i
 
 int attn_decode_splits(int max_ctx) { return (max_ctx + kAttnSplitLen - 1) / kAttnSplitLen; }
 
-int attn_decode_launch(const float* q, const void* k_cache, const void* v_cache, float* part, float* out,
-                       int n_heads, int n_kv, int hd, const int* pos_ptr, int max_ctx, hipStream_t st) {
+int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx) {
+    return (int64_t)n_heads * attn_decode_splits(max_ctx) * (hd + 2);
+}
+
+int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* part, float* out, int n_heads,
+                       int n_kv, int hd, const int* pos_ptr, int max_ctx, bool rope, float theta, hipStream_t st) {
     if (n_kv <= 0 || n_heads % n_kv) return fail(kInvalidArgument, "attention: n_heads %% n_kv_heads != 0");
     const int splits = attn_decode_splits(max_ctx);
-    dim3 grid(n_heads, splits);
+    if (splits > 64)
+        return fail(kUnsupported, "attention: max_ctx %d exceeds %d positions", max_ctx, 64 * kAttnSplitLen);
+    if ((uintptr_t)qkv % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
+        return fail(kInvalidArgument, "attention: q and the caches must be 16-byte aligned");
+    const dim3 grid(n_heads, splits);
+    __half* kc = (__half*)k_cache;
+    __half* vc = (__half*)v_cache;
     if (hd == 128) {
-        hipLaunchKernelGGL((attn_decode_partial<128>), grid, dim3(kBlock), 0, st, q, (const __half*)k_cache,
-                           (const __half*)v_cache, part, n_heads, n_kv, pos_ptr, max_ctx, kAttnSplitLen);
-        hipLaunchKernelGGL((attn_decode_combine<128>), dim3(n_heads), dim3(128), 0, st, part, out, splits);
+        if (rope)
+            hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                               n_heads, n_kv, pos_ptr, max_ctx, theta);
+        else
+            hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                               n_heads, n_kv, pos_ptr, max_ctx, theta);
+        hipLaunchKernelGGL((attn_decode_merge<128>), dim3(n_heads), dim3(128), 0, st, part, out, splits);
     } else if (hd == 64) {
-        hipLaunchKernelGGL((attn_decode_partial<64>), grid, dim3(kBlock), 0, st, q, (const __half*)k_cache,
-                           (const __half*)v_cache, part, n_heads, n_kv, pos_ptr, max_ctx, kAttnSplitLen);
-        hipLaunchKernelGGL((attn_decode_combine<64>), dim3(n_heads), dim3(64), 0, st, part, out, splits);
+        if (rope)
+            hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                               n_heads, n_kv, pos_ptr, max_ctx, theta);
+        else
+            hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                               n_heads, n_kv, pos_ptr, max_ctx, theta);
+        hipLaunchKernelGGL((attn_decode_merge<64>), dim3(n_heads), dim3(64), 0, st, part, out, splits);
     } else {
         return fail(kUnsupported, "attention: head_dim %d (supported: 64, 128)", hd);
     }

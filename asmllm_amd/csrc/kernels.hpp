@@ -69,12 +69,14 @@ int attention_launch(const float* q, const float* k, const float* v, float* y, i
                      hipStream_t st);
 
 // Decode attention over head-major fp16 caches [n_kv][max_ctx][hd], positions
-// 0..*pos_ptr; split into kAttnSplitLen-position chunks, combined in a second
-// kernel.  `part` holds n_heads * attn_decode_splits(max_ctx) * (hd + 2) floats.
+// 0..*pos_ptr: kAttnSplitLen-position splits, then a merge launch.  `part`
+// holds attn_decode_workspace() floats.  rope = true rotates q and the new k
+// at *pos_ptr and writes the new k/v rows (fp16) in the split launch.
 constexpr int kAttnSplitLen = 128;
 int attn_decode_splits(int max_ctx);
-int attn_decode_launch(const float* q, const void* k_cache, const void* v_cache, float* part, float* out,
-                       int n_heads, int n_kv, int hd, const int* pos_ptr, int max_ctx, hipStream_t st);
+int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx);
+int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* part, float* out, int n_heads,
+                       int n_kv, int hd, const int* pos_ptr, int max_ctx, bool rope, float theta, hipStream_t st);
 
 int embed_q4_0_launch(const void* table, const int* token, float* x, int n_vocab, int dim, hipStream_t st);
 int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st);

@@ -17,6 +17,8 @@ stream, so it can be captured once into a HIP graph and replayed per token:
     reads the token, RoPE / the KV write / attention read the position, and
     the argmax kernel writes the next token and advances the position, so a
     replayed graph walks the sequence without host involvement;
+  * RoPE and the KV-cache write are fused into the attention launch
+    (asmhip_attention_decode_rope);
   * the KV cache is fp16, head-major [n_kv_heads][max_ctx][head_dim] per layer
     (the reference keeps fp32 [128][heads][head_dim], generate.py:252-253).
 
@@ -197,11 +199,9 @@ class DecodeEngine:
         check(L.asmhip_embed_q4_0(self.embed.ptr, self.token.ptr, self.x.ptr, s.vocab, d, st), "embed")
         for ly in self.layers:
             mv(ly.wqkv, self.x, self.qkv.ptr, s.qkv_rows, d, RMS, ly.attn_norm.ptr, 0, "qkv matvec")
-            check(L.asmhip_rope_kv_write(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr, s.n_heads, s.n_kv_heads, hd,
-                                         self.pos.ptr, self.max_ctx, ctypes.c_float(s.theta), st), "rope/kv write")
-            check(L.asmhip_attention_decode(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr, self.workspace.ptr,
-                                            self.attn.ptr, s.n_heads, s.n_kv_heads, hd, self.pos.ptr, self.max_ctx,
-                                            st), "attention")
+            check(L.asmhip_attention_decode_rope(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr, self.workspace.ptr,
+                                                 self.attn.ptr, s.n_heads, s.n_kv_heads, hd, self.pos.ptr,
+                                                 self.max_ctx, ctypes.c_float(s.theta), st), "rope + attention")
             mv(ly.wo, self.attn, self.x.ptr, d, d, NONE, None, 1, "o matvec")
             mv(ly.wgu, self.x, self.gu.ptr, 2 * h, d, RMS, ly.ffn_norm.ptr, 0, "gate/up matvec")
             mv(ly.wdown, self.gu, self.x.ptr, d, h, SWI, self.gu.ptr + 4 * h, 1, "down matvec")

@@ -205,24 +205,36 @@ def _rotating_blocks(qtype: int, M: int, K: int, copies: int, seed: int):
     return bufs, nbytes
 
 
+EAGER = False  # --eager: launch directly instead of replaying graphs
+
+
 def time_launches(enqueue, copies: int, reps: int) -> float:
     """Mean GPU microseconds of one launch: `enqueue(i)` for i < copies captured
     into one graph, replayed `reps` times between HIP events."""
     from asmllm_amd.device import Event, Graph, Stream, synchronize
 
     stream = Stream()
-    graph = Graph.capture(stream, lambda: [enqueue(i, stream.handle) for i in range(copies)])
+    if EAGER:
+        def run():
+            for i in range(copies):
+                enqueue(i, stream.handle)
+    else:
+        graph = Graph.capture(stream, lambda: [enqueue(i, stream.handle) for i in range(copies)])
+
+        def run():
+            graph.launch(stream)
     for _ in range(2):
-        graph.launch(stream)
+        run()
     synchronize()
     e0, e1 = Event(), Event()
     e0.record(stream)
     for _ in range(reps):
-        graph.launch(stream)
+        run()
     e1.record(stream)
     e1.synchronize()
     us = e0.elapsed_ms(e1) * 1e3 / (reps * copies)
-    graph.close()
+    if not EAGER:
+        graph.close()
     return us
 
 
@@ -312,28 +324,36 @@ def bench_gemm(T: int = 512, M: int = 11008, K: int = 4096, copies: int = 12) ->
             "bytes": nbytes}
 
 
-def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4) -> dict:
+def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: bool = False) -> dict:
     """Greedy single-token decode of the 32-layer 7B-shape Q4_0 model, fp16 KV
     cache prefilled to `context`: `steps` tokens from position `context`,
     each one replay of the captured token-step graph (token and position stay
-    on the GPU between steps)."""
+    on the GPU between steps).  `eager` enqueues the launches directly instead
+    (for tracing tools that do not follow graph launches)."""
     from asmllm_amd.device import Event, synchronize
     from asmllm_amd.engine import LLAMA_7B, DecodeEngine
 
     s = LLAMA_7B
     eng = DecodeEngine(s, max_ctx=context + steps)
     eng.init_random(seed=42)
-    graph = eng.capture()
+    if eager:
+        step = eng.enqueue_step
+    else:
+        graph = eng.capture()
+
+        def step():
+            graph.launch(eng.stream)
+
     eng.set_position(1, context)
     for _ in range(warmup):
-        graph.launch(eng.stream)
+        step()
     eng.stream.synchronize()
     eng.set_position(1, context)
     synchronize()
     e0, e1 = Event(), Event()
     e0.record(eng.stream)
     for _ in range(steps):
-        graph.launch(eng.stream)
+        step()
     e1.record(eng.stream)
     e1.synchronize()
     ms = e0.elapsed_ms(e1)
@@ -349,7 +369,7 @@ def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4) -> dict
     log(f"decode: {tok_s:.1f} tokens/s ({ms / steps:.3f} ms/token)")
     return {"workload": f"7B-shape Q4_0 Llama greedy decode, {s.n_layers} layers, d {s.dim}, {s.n_heads}x"
                         f"{s.head_dim} heads, FFN {s.hidden_dim}, vocab {s.vocab}, fp16 KV prefilled to {context}",
-            "tokens_per_s": round(tok_s, 2), "ms_per_token": round(ms / steps, 4), "steps": steps,
+            "launch": "eager" if eager else "graph", "tokens_per_s": round(tok_s, 2), "ms_per_token": round(ms / steps, 4), "steps": steps,
             "context": context, "bytes_per_token": int(per_token),
             "GBps": round(per_token * tok_s / 1e9, 1), "frac": round(per_token * tok_s / 1e9 / HBM_PEAK_GBPS, 4)}
 
@@ -458,6 +478,7 @@ def main() -> None:
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-extra", action="store_true", help="skip the shape table, GEMM and decode legs")
     ap.add_argument("--only", choices=["decode", "gemm", "table"], help="run one extra leg and print its JSON")
+    ap.add_argument("--eager", action="store_true", help="with --only: launch without graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build has no multi-GPU path)",
@@ -471,8 +492,13 @@ def main() -> None:
     from asmllm_amd.device import device_info
 
     if args.only:
-        leg = {"decode": bench_decode, "gemm": bench_gemm, "table": bench_matvec_table}[args.only]
-        print(json.dumps({args.only: leg()}), flush=True)
+        global EAGER
+        EAGER = args.eager
+        if args.only == "decode":
+            res = bench_decode(eager=args.eager)
+        else:
+            res = {"gemm": bench_gemm, "table": bench_matvec_table}[args.only]()
+        print(json.dumps({args.only: res}), flush=True)
         return
 
     info = device_info()

@@ -174,14 +174,21 @@ ASMHIP_API int asmhip_attention(const float* q, const float* k, const float* v, 
  * place and writes rotated k and v at position *pos_dev.
  * asmhip_attention_decode computes, per head h (kv head h / (n_heads /
  * n_kv_heads)), softmax(q_h . k_p / sqrt(head_dim)) . v_p over positions
- * 0..*pos_dev; workspace holds asmhip_attention_decode_workspace() floats.
- * head_dim 64 or 128. */
+ * 0..*pos_dev (max_ctx <= 8192); workspace holds
+ * asmhip_attention_decode_workspace() floats (calls sharing one workspace
+ * must not overlap).  head_dim 64 or 128. */
 ASMHIP_API int asmhip_rope_kv_write(float* qkv, void* k_cache, void* v_cache, int n_heads, int n_kv_heads,
                                     int head_dim, const int* pos_dev, int max_ctx, float theta, void* stream);
 ASMHIP_API int64_t asmhip_attention_decode_workspace(int n_heads, int head_dim, int max_ctx);
 ASMHIP_API int asmhip_attention_decode(const float* q, const void* k_cache, const void* v_cache, float* workspace,
                                        float* out, int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
                                        int max_ctx, void* stream);
+/* Both of the above fused: q and the new k rotated at *pos_dev, the
+ * new k and v rows written to the caches (fp16), attention over 0..*pos_dev
+ * into out; q in qkv is left unrotated (generate.py:282-296). */
+ASMHIP_API int asmhip_attention_decode_rope(const float* qkv, void* k_cache, void* v_cache, float* workspace,
+                                            float* out, int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
+                                            int max_ctx, float theta, void* stream);
 /* x = row *token_dev of a Q4_0 embedding table [n_vocab][dim]
  * (generate.py:262, the table dequantized by get_tensor :169-182). */
 ASMHIP_API int asmhip_embed_q4_0(const void* table, const int* token_dev, float* x, int n_vocab, int dim,

@@ -120,6 +120,7 @@ def test_multi_head_rope_reads_position_on_device(hip, oracle):
 
 @pytest.mark.parametrize("n_heads,n_kv,hd,pos,max_ctx", [
     (32, 32, 128, 0, 256), (32, 32, 128, 2047, 2176), (32, 8, 128, 700, 1024), (8, 2, 64, 129, 130),
+    (32, 8, 128, 128, 300), (4, 4, 128, 127, 128), (8, 8, 64, 8191, 8192),
 ])
 def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos, max_ctx):
     rng = np.random.default_rng(n_heads * 1000 + pos)
@@ -134,6 +135,11 @@ def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos,
     ws = hip.asmhip_attention_decode_workspace(n_heads, hd, max_ctx)
     assert ws > 0
     dws, dout = DeviceBuffer(ws * 4), DeviceBuffer(n_heads * hd * 4)
+    # the fused form on copies of the same inputs
+    fqkv, fkc, fvc = DeviceBuffer.from_numpy(qkv), DeviceBuffer.from_numpy(kc), DeviceBuffer.from_numpy(vc)
+    fout = DeviceBuffer(n_heads * hd * 4)
+    _ok(hip, hip.asmhip_attention_decode_rope(fqkv.ptr, fkc.ptr, fvc.ptr, dws.ptr, fout.ptr, n_heads, n_kv, hd,
+                                              dpos.ptr, max_ctx, 10000.0, None))
     _ok(hip, hip.asmhip_rope_kv_write(dqkv.ptr, dkc.ptr, dvc.ptr, n_heads, n_kv, hd, dpos.ptr, max_ctx, 10000.0,
                                       None))
     _ok(hip, hip.asmhip_attention_decode(dqkv.ptr, dkc.ptr, dvc.ptr, dws.ptr, dout.ptr, n_heads, n_kv, hd,
@@ -159,7 +165,14 @@ def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos,
     kc_o = np.ascontiguousarray(got_kc.transpose(1, 0, 2)).view(np.uint16)
     vc_o = np.ascontiguousarray(got_vc.transpose(1, 0, 2)).view(np.uint16)
     ref = oracle.attention_decode_f16(got_q, kc_o, vc_o, pos + 1, n_kv, 8)
-    np.testing.assert_allclose(dout.download(np.float32, (n_heads, hd)), ref, rtol=TOL, atol=TOL)
+    out = dout.download(np.float32, (n_heads, hd))
+    np.testing.assert_allclose(out, ref, rtol=TOL, atol=TOL)
+    # fused = rope_kv_write then attention, bit for bit (same rotation, same fp16 row)
+    np.testing.assert_array_equal(fout.download(np.float32, (n_heads, hd)), out)
+    np.testing.assert_array_equal(fkc.download(np.float16, (n_kv, max_ctx, hd)), got_kc)
+    np.testing.assert_array_equal(fvc.download(np.float16, (n_kv, max_ctx, hd)), got_vc)
+    np.testing.assert_array_equal(fqkv.download(np.float32, qkv.size), qkv)  # q left unrotated
+
 
 
 def test_embed_row_and_argmax(hip, oracle):
