@@ -324,7 +324,53 @@ def bench_gemm(T: int = 512, M: int = 11008, K: int = 4096, copies: int = 12) ->
             "bytes": nbytes}
 
 
-def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: bool = False) -> dict:
+def decode_cpu_baseline(eng, context: int, seconds: float) -> dict:
+    """The oracle's decode step (the reference's forward_token sequence over the
+    oracle's restated kernels, generate.py:261-326) on the host cores, on the
+    engine's own weights and cache read back from HBM: tokens from position
+    `context` until `seconds` have passed (at least two)."""
+    from oracle.decode_ref import DecodeRef
+
+    s = eng.shape
+    d, h, kv = s.dim, s.hidden_dim, s.kv_dim
+
+    def blocks(buf, rows, K):
+        return buf.download(np.uint8, (rows, K // 32, 18))
+
+    layers, kcs, vcs = [], [], []
+    for ly in eng.layers:
+        qkv, gu = blocks(ly.wqkv, s.qkv_rows, d), blocks(ly.wgu, 2 * h, d)
+        layers.append({"attn_norm": ly.attn_norm.download(np.float32, d),
+                       "ffn_norm": ly.ffn_norm.download(np.float32, d),
+                       "wq": qkv[:d], "wk": qkv[d:d + kv], "wv": qkv[d + kv:], "wo": blocks(ly.wo, d, d),
+                       "w_gate": gu[:h], "w_up": gu[h:], "w_down": blocks(ly.wdown, d, h)})
+        kcs.append(ly.k_cache.download(np.uint16, (s.n_kv_heads, eng.max_ctx, s.head_dim)))
+        vcs.append(ly.v_cache.download(np.uint16, (s.n_kv_heads, eng.max_ctx, s.head_dim)))
+    cores = host_cores()
+    ref = DecodeRef(dim=d, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, hidden_dim=h, vocab=s.vocab, eps=s.eps,
+                    theta=s.theta, embed=blocks(eng.embed, s.vocab, d),
+                    final_norm=eng.final_norm.download(np.float32, d), output=blocks(eng.output, s.vocab, d),
+                    layers=layers, k_caches=kcs, v_caches=vcs, nt=cores)
+    del kcs, vcs
+    token, times = 1, []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 2 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        logits = ref.forward_token(token, context + len(times))
+        times.append(time.perf_counter() - t0)
+        token = int(np.argmax(logits))
+    from oracle import native as oracle
+
+    oracle.threadpool_shutdown()
+    med = float(np.median(times))
+    return {"value": round(1.0 / med, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"{len(times)} greedy decode tokens of the same 7B-shape model from position {context}: "
+                       f"oracle forward_token (restated AVX2 Q4_0 kernel + threadpool tiling over GGUF blocks, "
+                       f"fp16-cache attention) on {cores} threads, median {med:.3f} s per token")}
+
+
+def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: bool = False,
+                 cpu_seconds: float = 0.0) -> dict:
     """Greedy single-token decode of the 32-layer 7B-shape Q4_0 model, fp16 KV
     cache prefilled to `context`: `steps` tokens from position `context`,
     each one replay of the captured token-step graph (token and position stay
@@ -365,13 +411,15 @@ def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: 
     kv_read = sum((p + 1) for p in range(context, context + steps)) / steps * s.kv_bytes_per_position()
     per_token = s.weight_bytes() + (s.dim // 32) * 18 + kv_read + s.kv_bytes_per_position()
     tok_s = steps / (ms / 1e3)
+    cpu = decode_cpu_baseline(eng, context, cpu_seconds) if cpu_seconds > 0 else None
     eng.close()
     log(f"decode: {tok_s:.1f} tokens/s ({ms / steps:.3f} ms/token)")
     return {"workload": f"7B-shape Q4_0 Llama greedy decode, {s.n_layers} layers, d {s.dim}, {s.n_heads}x"
                         f"{s.head_dim} heads, FFN {s.hidden_dim}, vocab {s.vocab}, fp16 KV prefilled to {context}",
             "launch": "eager" if eager else "graph", "tokens_per_s": round(tok_s, 2), "ms_per_token": round(ms / steps, 4), "steps": steps,
             "context": context, "bytes_per_token": int(per_token),
-            "GBps": round(per_token * tok_s / 1e9, 1), "frac": round(per_token * tok_s / 1e9 / HBM_PEAK_GBPS, 4)}
+            "GBps": round(per_token * tok_s / 1e9, 1), "frac": round(per_token * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
+            "cpu_baseline": cpu}
 
 
 def profile_pass(copies: int, launches: int = 64) -> None:
@@ -495,7 +543,7 @@ def main() -> None:
         global EAGER
         EAGER = args.eager
         if args.only == "decode":
-            res = bench_decode(eager=args.eager)
+            res = bench_decode(eager=args.eager, cpu_seconds=0.0 if args.no_cpu else args.cpu_seconds)
         else:
             res = {"gemm": bench_gemm, "table": bench_matvec_table}[args.only]()
         print(json.dumps({args.only: res}), flush=True)
@@ -507,7 +555,7 @@ def main() -> None:
     achieved = mv["bytes_per_step"] / (mv["kernel_us_mean"] * 1e-6) / 1e9
     extra = {}
     if not args.no_extra:
-        extra["decode"] = bench_decode()
+        extra["decode"] = bench_decode(cpu_seconds=0.0 if args.no_cpu else args.cpu_seconds)
         extra["gemm"] = bench_gemm()
         extra["matvec_table"] = bench_matvec_table()
     cpu = None if args.no_cpu else bench_cpu_baseline(args.cpu_seconds)

@@ -25,7 +25,8 @@ from . import native as o
 
 class DecodeRef:
     """Host copy of a decode model: GGUF Q4_0 blocks ([rows][K/32][18] uint8),
-    fp32 norm weights, fp16 caches [n_kv][max_ctx][hd] as uint16 bits."""
+    fp32 norm weights, fp16 caches given head-major [n_kv][max_ctx][hd] as
+    uint16 bits (stored position-major in k_caches / v_caches)."""
 
     def __init__(self, *, dim, n_heads, n_kv_heads, hidden_dim, vocab, eps, theta, embed, final_norm, output,
                  layers, k_caches, v_caches, nt: int = 1):
@@ -34,8 +35,10 @@ class DecodeRef:
         self.hd = dim // n_heads
         self.embed, self.final_norm, self.output = embed, final_norm, output
         self.layers = layers            # dicts: attn_norm wq wk wv wo ffn_norm w_gate w_up w_down
-        self.k_caches = [np.array(k, np.uint16) for k in k_caches]
-        self.v_caches = [np.array(v, np.uint16) for v in v_caches]
+        # kept position-major [max_ctx][n_kv][hd], the oracle kernel's layout, so a
+        # step slices the cache without copying it
+        self.k_caches = [np.ascontiguousarray(np.asarray(k, np.uint16).transpose(1, 0, 2)) for k in k_caches]
+        self.v_caches = [np.ascontiguousarray(np.asarray(v, np.uint16).transpose(1, 0, 2)) for v in v_caches]
         self.nt = nt
 
     def _mv(self, blocks, x):
@@ -61,12 +64,10 @@ class DecodeRef:
             q = self._rope_heads(q, nh)                                           # :282-285
             k = self._rope_heads(k, nkv)
             kc, vc = self.k_caches[li], self.v_caches[li]                         # :289-290
-            kc[:, pos, :] = k.reshape(nkv, hd).astype(np.float16).view(np.uint16)
-            vc[:, pos, :] = v.reshape(nkv, hd).astype(np.float16).view(np.uint16)
-            # position-major view [pos][n_kv][hd] for the oracle kernel
-            kp = np.ascontiguousarray(kc[:, :pos + 1, :].transpose(1, 0, 2))
-            vp = np.ascontiguousarray(vc[:, :pos + 1, :].transpose(1, 0, 2))
-            attn = o.attention_decode_f16(q.reshape(nh, hd), kp, vp, pos + 1, nkv, self.nt)   # :291-296
+            kc[pos] = k.reshape(nkv, hd).astype(np.float16).view(np.uint16)
+            vc[pos] = v.reshape(nkv, hd).astype(np.float16).view(np.uint16)
+            attn = o.attention_decode_f16(q.reshape(nh, hd), kc[:pos + 1], vc[:pos + 1], pos + 1, nkv,
+                                          self.nt)                                # :291-296
             x = x + self._mv(ly["wo"], attn.reshape(-1))                          # :298-300
             xn = o.rmsnorm(x, ly["ffn_norm"], self.eps)                           # :302-306
             gate = self._mv(ly["w_gate"], xn)                                     # :308-311

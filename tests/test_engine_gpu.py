@@ -76,11 +76,12 @@ def test_decode_steps_match_oracle(shape):
         print(f"step {step}: max err / max|logit| {rel:.2e}")
         token = int(np.argmax(want))
     # the caches agree after the steps: k within one fp16 rounding, v likewise
+    s = eng.shape
     for li, ly in enumerate(eng.layers):
-        kc = ly.k_cache.download(np.uint16, ref.k_caches[li].shape)
+        kc = ly.k_cache.download(np.uint16, (s.n_kv_heads, eng.max_ctx, s.head_dim))
         for p in range(pos0, pos0 + 4):
             a = kc[:, p].view(np.float16).astype(np.float32)
-            b = ref.k_caches[li][:, p].view(np.float16).astype(np.float32)
+            b = ref.k_caches[li][p].view(np.float16).astype(np.float32)   # oracle keeps [pos][kv][hd]
             np.testing.assert_allclose(a, b, rtol=2 ** -9, atol=1e-3)
     eng.close()
 
