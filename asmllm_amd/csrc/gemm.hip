@@ -213,7 +213,7 @@ struct RawStep {
     static constexpr int kRows = kTT + kTM;
     static constexpr int kTotal = kRows * kPieces;
     static constexpr int kPerThread = (kTotal + kThreadsG - 1) / kThreadsG;
-    static constexpr int kBytes = kRows * kPitch;
+    static constexpr int kStage = kRows * kPitch + 16;             // + spare dwords for dead slots
 };
 
 // 16 qs bytes of block BLK (of a dword-aligned pair) for lane group g: an odd
@@ -242,51 +242,63 @@ __device__ __forceinline__ v4h raw_scale(const uint8_t* row) {
     return v;
 }
 
-template <int KB>
+template <int KB, int D>
 __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* __restrict__ w,
                                                                  const uint8_t* __restrict__ a,
-                                                                 float* __restrict__ c, int T, int M, int K) {
+                                                                 float* __restrict__ c, int T, int M, int K,
+                                                                 int tiles_t, int n_tiles) {
     using S = RawStep<KB>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    // XCD-aware tile order: workgroup ids are dealt round-robin to the 8 XCDs,
+    // so id -> (xcd = id % 8, j = id / 8) -> tile xcd * chunk + j gives each XCD
+    // a run of consecutive tiles, T fastest: the T tiles sharing a weight tile
+    // meet in one L2.  The grid is padded to a multiple of 8; extra ids exit.
+    const int chunk = (int)gridDim.x >> 3;
+    const int tile = ((int)blockIdx.x & 7) * chunk + ((int)blockIdx.x >> 3);
+    if (tile >= n_tiles) return;
     const int nb = K >> 5;
     const uint32_t row_bytes = (uint32_t)nb * 34u;
-    const int t0 = blockIdx.y * kTT, j0 = blockIdx.x * kTM;
+    const int t0 = (tile % tiles_t) * kTT, j0 = (tile / tiles_t) * kTM;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wt = wave >> 1, wm = wave & 1;
     const auto ar = make_rsrc(a, row_bytes * (uint32_t)T);
     const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
 
-    // piece q = (staged row q / kPieces, 16-byte piece q % kPieces); A rows first
+    // piece q = (staged row q / kPieces, 16-byte piece q % kPieces); A rows first.
+    // Slots past the last piece load from past the buffer (zeros, no access) and
+    // park in the stage's spare dwords.
     uint32_t goff[S::kPerThread], loff[S::kPerThread];
-    bool is_a[S::kPerThread], live[S::kPerThread];
+    bool is_a[S::kPerThread];
 #pragma unroll
     for (int i = 0; i < S::kPerThread; ++i) {
         const int q = (int)threadIdx.x + kThreadsG * i;
-        live[i] = q < S::kTotal;
-        const int qq = live[i] ? q : 0;
+        const bool live = q < S::kTotal;
+        const int qq = live ? q : 0;
         const int r = qq / S::kPieces, k = qq - r * S::kPieces;
         is_a[i] = r < kTT;
         const int grow = is_a[i] ? t0 + r : j0 + (r - kTT);
-        goff[i] = (uint32_t)grow * row_bytes + 16u * (uint32_t)k;
-        loff[i] = (uint32_t)(r * S::kPitch + 16 * k);
+        goff[i] = live ? (uint32_t)grow * row_bytes + 16u * (uint32_t)k : kPastEnd;
+        loff[i] = live ? (uint32_t)(r * S::kPitch + 16 * k) : (uint32_t)(S::kRows * S::kPitch);
     }
-    uint4 pre[S::kPerThread];
-    auto fetch = [&](int kb0) {
+    uint4 pre[D][S::kPerThread];
+    auto fetch = [&](uint4* dst, int kb0) {
+        const uint32_t kofs = (uint32_t)kb0 * 34u;
 #pragma unroll
-        for (int i = 0; i < S::kPerThread; ++i)
-            if (live[i]) pre[i] = buf_load_b128(is_a[i] ? ar : wr, goff[i] + (uint32_t)kb0 * 34u);
+        for (int i = 0; i < S::kPerThread; ++i) {
+            const uint32_t off = goff[i] == kPastEnd ? kPastEnd : goff[i] + kofs;
+            dst[i] = buf_load_b128(is_a[i] ? ar : wr, off);
+        }
     };
-    auto park = [&](uint8_t* stage) {
+    auto park = [&](const uint4* src, uint8_t* stage) {
 #pragma unroll
-        for (int i = 0; i < S::kPerThread; ++i)
-            if (live[i]) {
-                uint32_t* d = reinterpret_cast<uint32_t*>(stage + loff[i]);  // 4-byte aligned
-                d[0] = pre[i].x;
-                d[1] = pre[i].y;
-                d[2] = pre[i].z;
-                d[3] = pre[i].w;
-            }
+        for (int i = 0; i < S::kPerThread; ++i) {
+            uint32_t* d = reinterpret_cast<uint32_t*>(stage + loff[i]);  // 4-byte aligned
+            d[0] = src[i].x;
+            d[1] = src[i].y;
+            d[2] = src[i].z;
+            d[3] = src[i].w;
+        }
     };
 
     const int m = lane & 31, g = lane >> 5;
@@ -297,42 +309,49 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* 
         for (int i = 0; i < 16; ++i) acc[nt][i] = 0.f;
 
     const int nsteps = nb / KB;
-    fetch(0);
-    for (int s = 0; s < nsteps; ++s) {
-        uint8_t* stage = lds + (s & 1) * S::kBytes;
-        park(stage);
-        __syncthreads();
-        if (s + 1 < nsteps) fetch((s + 1) * KB);
-        const uint8_t* arow = stage + (32 * wt + m) * S::kPitch;
-        const uint8_t* wrow0 = stage + (kTT + 64 * wm + m) * S::kPitch;
-        const uint8_t* wrow1 = wrow0 + 32 * S::kPitch;
-        // block BLK (0 or 1) of the dword-aligned pair at byte 68 bp
-        auto block = [&](auto blk_c, int bp) {
-            constexpr int BLK = decltype(blk_c)::value;
-            const uint8_t* ar_ = arow + 68 * bp;
-            const uint8_t* w0_ = wrow0 + 68 * bp;
-            const uint8_t* w1_ = wrow1 + 68 * bp;
-            const v4i av = raw_qs<BLK>(ar_, g);
-            const v4h da = raw_scale<BLK>(ar_);
-            const v4i bv0 = raw_qs<BLK>(w0_, g);
-            const v4h dw0 = raw_scale<BLK>(w0_);
-            const v4i bv1 = raw_qs<BLK>(w1_, g);
-            const v4h dw1 = raw_scale<BLK>(w1_);
-            const v16i zi = {};
-            const v16f zf = {};
-            const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv0, zi, 0, 0, 0);
-            const v16f s0 = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw0, zf, 0, 0, 0);  // 2 d_a d_w
-            const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv1, zi, 0, 0, 0);
-            const v16f s1 = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw1, zf, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[0][i] = fmaf((float)d0[i], s0[i], acc[0][i]);
+    for (int u = 0; u < D; ++u)
+        if (u < nsteps) fetch(pre[u], u * KB);
+    for (int s0 = 0; s0 < nsteps; s0 += D) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[1][i] = fmaf((float)d1[i], s1[i], acc[1][i]);
-        };
+        for (int u = 0; u < D; ++u) {
+            const int s = s0 + u;
+            if (s >= nsteps) break;
+            uint8_t* stage = lds + (s & 1) * S::kStage;
+            park(pre[u], stage);
+            __syncthreads();
+            if (s + D < nsteps) fetch(pre[u], (s + D) * KB);
+            const uint8_t* arow = stage + (32 * wt + m) * S::kPitch;
+            const uint8_t* wrow0 = stage + (kTT + 64 * wm + m) * S::kPitch;
+            const uint8_t* wrow1 = wrow0 + 32 * S::kPitch;
+            // block BLK (0 or 1) of the dword-aligned pair at byte 68 bp
+            auto block = [&](auto blk_c, int bp) {
+                constexpr int BLK = decltype(blk_c)::value;
+                const uint8_t* ar_ = arow + 68 * bp;
+                const uint8_t* w0_ = wrow0 + 68 * bp;
+                const uint8_t* w1_ = wrow1 + 68 * bp;
+                const v4i av = raw_qs<BLK>(ar_, g);
+                const v4h da = raw_scale<BLK>(ar_);
+                const v4i bv0 = raw_qs<BLK>(w0_, g);
+                const v4h dw0 = raw_scale<BLK>(w0_);
+                const v4i bv1 = raw_qs<BLK>(w1_, g);
+                const v4h dw1 = raw_scale<BLK>(w1_);
+                const v16i zi = {};
+                const v16f zf = {};
+                const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv0, zi, 0, 0, 0);
+                const v16f s0 = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw0, zf, 0, 0, 0);  // 2 d_a d_w
+                const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv1, zi, 0, 0, 0);
+                const v16f s1 = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw1, zf, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[0][i] = fmaf((float)d0[i], s0[i], acc[0][i]);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[1][i] = fmaf((float)d1[i], s1[i], acc[1][i]);
+            };
 #pragma unroll 1
-        for (int bp = 0; bp < KB / 2; ++bp) {
-            block(std::integral_constant<int, 0>{}, bp);
-            block(std::integral_constant<int, 1>{}, bp);
+            for (int bp = 0; bp < KB / 2; ++bp) {
+                block(std::integral_constant<int, 0>{}, bp);
+                block(std::integral_constant<int, 1>{}, bp);
+            }
         }
     }
 
@@ -348,6 +367,12 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* 
     }
 }
 
+// Two blocks per staged K step, one step of loads in flight per thread.
+// Deeper register rings (2-4 steps) and 4- or 8-block steps measured slower on
+// MI355X: the extra registers cost occupancy, which this VALU-bound loop needs.
+constexpr int kGemmKB = 2;  // blocks per staged K step (even)
+constexpr int kGemmD = 1;   // K steps of loads in flight per thread
+
 }  // namespace
 
 int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t M, int64_t K, hipStream_t st) {
@@ -360,13 +385,15 @@ int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t 
     if ((uintptr_t)w % 4 || (uintptr_t)a % 4) return fail(kInvalidArgument, "gemm: blocks must be 4-byte aligned");
     const dim3 grid((unsigned)((M + kTM - 1) / kTM), (unsigned)((T + kTT - 1) / kTT));
     if (grid.y > 65535) return fail(kInvalidArgument, "gemm: T too large");
-    if ((K / 32) % 2 == 0) {
-        constexpr int kKB = 2;
-        const size_t lds = 2 * (size_t)RawStep<kKB>::kBytes;
-        const int rc = dynamic_lds((const void*)gemm_q8_0_coalesced<kKB>, lds);
+    if ((K / 32) % kGemmKB == 0) {
+        const int tiles_t = (int)grid.y, n_tiles = (int)(grid.x * grid.y);
+        const unsigned padded = (unsigned)((n_tiles + 7) / 8 * 8);
+        const size_t lds = 2 * (size_t)RawStep<kGemmKB>::kStage;
+        const int rc = dynamic_lds((const void*)gemm_q8_0_coalesced<kGemmKB, kGemmD>, lds);
         if (rc) return rc;
-        hipLaunchKernelGGL((gemm_q8_0_coalesced<kKB>), grid, dim3(kThreadsG), lds, st, static_cast<const uint8_t*>(w),
-                           static_cast<const uint8_t*>(a), c, (int)T, (int)M, (int)K);
+        hipLaunchKernelGGL((gemm_q8_0_coalesced<kGemmKB, kGemmD>), dim3(padded), dim3(kThreadsG), lds, st,
+                           static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(a), c, (int)T, (int)M, (int)K,
+                           tiles_t, n_tiles);
     } else {
         // any K % 32 == 0: blocks staged one by one, qs realigned on the way into LDS
         constexpr int kKB = 4;
