@@ -33,9 +33,12 @@
 // beyond the buffer, which returns zeros without touching memory).  A unit is
 // parked in the wave's LDS slot and its MFMA operands are read back.  x is
 // digitized once per workgroup into LDS while the first loads are in flight.
-// Each wave keeps its per-tile partial sums in LDS; after the stream the
-// workgroup adds the NW partials of every row in a fixed order.  The main
-// loop has no workgroup barrier.
+// When every wave takes the same units of every tile (K = 4096: units w and
+// w + 8), a wave loads its A operands and block scales into registers once
+// and reuses them for every tile, which takes the x reads out of the per-unit
+// LDS traffic.  Each wave keeps its per-tile partial sums in LDS; after the
+// stream the workgroup adds the NW partials of every row in a fixed order.
+// The main loop has no workgroup barrier.
 #include <algorithm>
 
 #include "common.hpp"
@@ -92,14 +95,15 @@ __device__ __forceinline__ float block_value(v4i d) {
     return fmaf((float)hi, 65536.0f, (float)lo);
 }
 
-// Row n's dot with x over NB staged blocks (NB even), for the lane (n, g):
-// every operand is read from LDS first, then the MFMAs issue back to back,
-// then the per-block epilogues; no branch separates them.
+// Row n's dot with x over NB staged blocks (NB even), for the lane (n, g),
+// with the lane's A operands aq[] and block scales xs[] given: every weight
+// operand is read from LDS first, then the MFMAs issue back to back, then the
+// per-block epilogues; no branch separates them.
 template <int NB>
-__device__ __forceinline__ float chunk_dot(const uint8_t* rowd, const uint8_t* rowp, const uint8_t* xa,
-                                           const float* xs, float acc) {
+__device__ __forceinline__ float chunk_dot_x(const uint8_t* rowd, const uint8_t* rowp, const long* aq,
+                                             const float* xs, float acc) {
     constexpr int NP = NB / 2;
-    long bq[NB], aq[NB];
+    long bq[NB];
     uint32_t sc[NP][2];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -112,8 +116,6 @@ __device__ __forceinline__ float chunk_dot(const uint8_t* rowd, const uint8_t* r
         // fp16 scales of the two blocks (low half, high half); the same for every lane group
         sc[p][0] = *reinterpret_cast<const uint32_t*>(rowd + 36 * p);
         sc[p][1] = *reinterpret_cast<const uint32_t*>(rowd + 36 * p + 16);
-        aq[2 * p] = *reinterpret_cast<const long*>(xa + (2 * p) * kXStride);
-        aq[2 * p + 1] = *reinterpret_cast<const long*>(xa + (2 * p + 1) * kXStride);
     }
     const v4i z = {0, 0, 0, 0};
     v4i d[NB];
@@ -128,7 +130,20 @@ __device__ __forceinline__ float chunk_dot(const uint8_t* rowd, const uint8_t* r
     return acc + acc1;
 }
 
-template <int XQ, int NW, int D>
+// The same with the A operands read from the x digits in LDS.
+template <int NB>
+__device__ __forceinline__ float chunk_dot(const uint8_t* rowd, const uint8_t* rowp, const uint8_t* xa,
+                                           const float* xs, float acc) {
+    long aq[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) aq[j] = *reinterpret_cast<const long*>(xa + j * kXStride);
+    return chunk_dot_x<NB>(rowd, rowp, aq, xs, acc);
+}
+
+// PW > 0: every wave streams exactly PW units of each tile (K = 256 NW PW), so
+// its x operands are the same for every tile and stay in registers; PW = 0:
+// any K, operands read from LDS per unit.
+template <int XQ, int NW, int D, int PW>
 __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int M, int K, int pre, const float* __restrict__ pre_arg,
@@ -284,6 +299,37 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
     const uint8_t* rowd = wbuf + n * kUnitRowBytes;  // row n's staged blocks (scales at 18 j)
     const uint8_t* rowp = rowd + 4 * g;              // this lane's qs dword
     float acc = 0.f;
+    if constexpr (PW > 0) {
+        static_assert(PW % D == 0, "a tile's units fill whole rounds of the load ring");
+        long aq[PW][kUnitBlocks];
+        float xsr[PW][kUnitBlocks];
+#pragma unroll
+        for (int j = 0; j < PW; ++j)
+#pragma unroll
+            for (int b = 0; b < kUnitBlocks; ++b) {
+                const int blk = (wave + NW * j) * kUnitBlocks + b;
+                aq[j][b] = *reinterpret_cast<const long*>(xdig + blk * kXStride + aoff);
+                xsr[j][b] = xscale[blk];
+            }
+        for (int i = 0; i < my_tiles; ++i) {
+#pragma unroll
+            for (int j = 0; j < PW; ++j) {
+                const int d = j % D, s = i * PW + j;
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    const int q = lane + 64 * k;
+                    if (q < kUnitPieces) *reinterpret_cast<uint4*>(wbuf + 16 * q) = buf[d][k];
+                }
+                __builtin_amdgcn_wave_barrier();
+                acc = chunk_dot_x<kUnitBlocks>(rowd, rowp, aq[j], xsr[j], acc);
+                __builtin_amdgcn_wave_barrier();
+                load_unit(buf[d], s + D);
+            }
+            const float acc2 = __shfl_down(acc, 16, 64);  // level 2 of row n
+            if (g == 0) part[(i * NW + wave) * 16 + n] = fmaf(acc2, 9.313225746154785e-10f, acc);  // 2^-30
+            acc = 0.f;
+        }
+    } else
     for (int s0 = 0; s0 < L; s0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
@@ -327,14 +373,14 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
 constexpr int kStreamWaves = 8;
 constexpr int kStreamDepth = 2;
 
-template <int XQ>
+template <int XQ, int PW>
 int launch_xq(const uint8_t* w, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
-    const void* fn = (const void*)q4_0_mfma_stream<XQ, kStreamWaves, kStreamDepth>;
+    const void* fn = (const void*)q4_0_mfma_stream<XQ, kStreamWaves, kStreamDepth, PW>;
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
-    hipLaunchKernelGGL((q4_0_mfma_stream<XQ, kStreamWaves, kStreamDepth>), dim3(grid), dim3(kStreamWaves * 64), lds,
-                       st, w, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate);
+    hipLaunchKernelGGL((q4_0_mfma_stream<XQ, kStreamWaves, kStreamDepth, PW>), dim3(grid), dim3(kStreamWaves * 64),
+                       lds, st, w, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate);
     return kOk;
 }
 
@@ -395,12 +441,15 @@ int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const int m = (int)M, k = (int)K;
     int rc;
-    if (xq <= 1)
-        rc = launch_xq<1>(wb, x, y, m, k, grid, lds, st, o);
+    const int nu = nb / kUnitBlocks;  // units per tile
+    if (nu == kStreamWaves * 2)  // K = 4096: two units per wave and tile, x operands in registers
+        rc = launch_xq<1, 2>(wb, x, y, m, k, grid, lds, st, o);
+    else if (xq <= 1)
+        rc = launch_xq<1, 0>(wb, x, y, m, k, grid, lds, st, o);
     else if (xq <= 2)
-        rc = launch_xq<2>(wb, x, y, m, k, grid, lds, st, o);
+        rc = launch_xq<2, 0>(wb, x, y, m, k, grid, lds, st, o);
     else
-        rc = launch_xq<4>(wb, x, y, m, k, grid, lds, st, o);  // nb <= 512: at most 4 items per thread
+        rc = launch_xq<4, 0>(wb, x, y, m, k, grid, lds, st, o);  // nb <= 512: at most 4 items per thread
     if (rc) return rc;
     ASMHIP_TRY(hipGetLastError());
     return kOk;
