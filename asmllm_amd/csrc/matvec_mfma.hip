@@ -31,7 +31,8 @@
 // sequence of units.  D units of loads stay in flight per wave (coalesced
 // 16-byte buffer loads; past the end of the sequence the offset is pushed
 // beyond the buffer, which returns zeros without touching memory).  A unit is
-// parked in the wave's LDS slot and its MFMA operands are read back.  x is
+// parked in the wave's LDS slot (rows at a 152-byte pitch, so the operand
+// reads are free of bank conflicts) and its MFMA operands are read back.  x is
 // digitized once per workgroup into LDS while the first loads are in flight.
 // When every wave takes the same units of every tile (K = 4096: units w and
 // w + 8), a wave loads its A operands and block scales into registers once
@@ -52,8 +53,13 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kUnitBlocks = 8;                     // blocks per unit
 constexpr int kUnitRowBytes = kUnitBlocks * 18;    // 144: one row's slice of a unit
-constexpr int kUnitBytes = 16 * kUnitRowBytes;     // 2304: LDS slot per wave
+constexpr int kUnitBytes = 16 * kUnitRowBytes;     // 2304 bytes of weights per unit
 constexpr int kUnitPieces = kUnitBytes / 16;       // 144 16-byte pieces: 3 loads per lane
+constexpr int kRowPitch = 152;                     // LDS bytes per staged row: 38 dwords, so the
+                                                   // operand reads of 16 rows x 2 lane groups hit
+                                                   // 32 distinct banks (a 144-byte pitch pairs rows
+                                                   // n and n + 8 on one bank)
+constexpr int kSlotBytes = 16 * kRowPitch;         // 2432: LDS slot per wave
 constexpr int kXStride = 264;                      // LDS bytes of x digits per block: [g][level*4+digit][8] + 8 pad
                                                    // (the pad staggers blocks across banks: conflict-free 8-byte writes)
 constexpr int kMaxBlocks = 512;                    // K <= 16384
@@ -61,6 +67,15 @@ constexpr int kMaxTilesPerGroup = 8;
 constexpr uint32_t kPastEnd = 0xFFFFFF00u;         // buffer offset that loads zeros
 
 static_assert(kUnitPieces <= 3 * 64, "a unit is three 16-byte loads per lane");
+
+// Piece q of a unit (row q / 9, bytes 16 (q % 9) of its 144-byte slice) into
+// the wave's LDS slot at the padded row pitch (8-byte aligned: two b64 stores).
+__device__ __forceinline__ void park_piece(uint8_t* wbuf, int q, uint4 v) {
+    const int r = q / 9, c = q - 9 * r;
+    uint2* dst = reinterpret_cast<uint2*>(wbuf + r * kRowPitch + 16 * c);
+    dst[0] = make_uint2(v.x, v.y);
+    dst[1] = make_uint2(v.z, v.w);
+}
 
 __device__ __forceinline__ long pack_q4(uint32_t q) {
     const uint32_t lo = ((q << 4) ^ 0x80808080u) & 0xF0F0F0F0u;  // bytes 16 (n_lo - 8)
@@ -161,8 +176,8 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
     const int per_w = wave < nu ? (nu - wave + NW - 1) / NW : 0;  // this wave's units per tile
     const int L = my_tiles * per_w;                              // length of this wave's stream
     const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
-    uint8_t* wbuf = lds + wave * kUnitBytes;
-    uint8_t* xdig = lds + NW * kUnitBytes;
+    uint8_t* wbuf = lds + wave * kSlotBytes;
+    uint8_t* xdig = lds + NW * kSlotBytes;
     float* xscale = reinterpret_cast<float*>(xdig + nb * kXStride);
     float* part = xscale + nb;  // [my_tiles][NW][16]
 
@@ -296,7 +311,7 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
     // 4) the stream: stage unit s, multiply, refill its buffer with unit s + D.
     const int n = lane & 15, g = lane >> 4;
     const int aoff = g * 64 + (n & 7) * 8;
-    const uint8_t* rowd = wbuf + n * kUnitRowBytes;  // row n's staged blocks (scales at 18 j)
+    const uint8_t* rowd = wbuf + n * kRowPitch;      // row n's staged blocks (scales at 18 j)
     const uint8_t* rowp = rowd + 4 * g;              // this lane's qs dword
     float acc = 0.f;
     if constexpr (PW > 0) {
@@ -318,7 +333,7 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
                     const int q = lane + 64 * k;
-                    if (q < kUnitPieces) *reinterpret_cast<uint4*>(wbuf + 16 * q) = buf[d][k];
+                    if (q < kUnitPieces) park_piece(wbuf, q, buf[d][k]);
                 }
                 __builtin_amdgcn_wave_barrier();
                 acc = chunk_dot_x<kUnitBlocks>(rowd, rowp, aq[j], xsr[j], acc);
@@ -338,7 +353,7 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
                     const int q = lane + 64 * k;
-                    if (q < kUnitPieces) *reinterpret_cast<uint4*>(wbuf + 16 * q) = buf[d][k];
+                    if (q < kUnitPieces) park_piece(wbuf, q, buf[d][k]);
                 }
                 __builtin_amdgcn_wave_barrier();
                 const int i = s / per_w;
@@ -398,7 +413,7 @@ StreamShape stream_shape(int64_t M, int64_t K) {
     StreamShape sh;
     sh.grid = std::max(std::min(n_tiles, compute_units()), (n_tiles + kMaxTilesPerGroup - 1) / kMaxTilesPerGroup);
     sh.tiles_per_group = (n_tiles + sh.grid - 1) / sh.grid;
-    sh.lds = (size_t)kStreamWaves * kUnitBytes + (size_t)nb * (kXStride + 4) +
+    sh.lds = (size_t)kStreamWaves * kSlotBytes + (size_t)nb * (kXStride + 4) +
              (size_t)sh.tiles_per_group * kStreamWaves * 16 * sizeof(float);
     return sh;
 }
