@@ -34,8 +34,8 @@
 // parked in the wave's LDS slot (rows at a 152-byte pitch, so the operand
 // reads are free of bank conflicts) and its MFMA operands are read back.  x is
 // digitized once per workgroup into LDS while the first loads are in flight.
-// When every wave takes the same units of every tile (K = 4096: units w and
-// w + 8), a wave loads its A operands and block scales into registers once
+// When every wave takes the same units of every tile (K = 4096 with 16 waves:
+// unit w), a wave loads its A operands and block scales into registers once
 // and reuses them for every tile, which takes the x reads out of the per-unit
 // LDS traffic.  Each wave keeps its per-tile partial sums in LDS; after the
 // stream the workgroup adds the NW partials of every row in a fixed order.
@@ -385,27 +385,50 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
     }
 }
 
-constexpr int kStreamWaves = 8;
-constexpr int kStreamDepth = 2;
+// Launch shapes.  The wide shape runs 16 waves with one unit of loads in
+// flight each (4 waves per SIMD interleave the per-unit LDS -> MFMA ->
+// epilogue chains); where its LDS does not fit (K above ~14K), 8 waves with
+// two units in flight each.  Both keep one 16-row tile of loads in flight per
+// CU: deeper streams (3-6 units per wave) measured slower on MI355X, the
+// extra requests queueing in the memory system (and delaying x) without
+// raising throughput.
+constexpr int kWideWaves = 16, kWideDepth = 1;
+constexpr int kNarrowWaves = 8, kNarrowDepth = 2;
+constexpr size_t kLdsBudget = 160 * 1024 - 256;
 
-template <int XQ, int PW>
+template <int XQ, int NW, int D, int PW>
 int launch_xq(const uint8_t* w, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
-    const void* fn = (const void*)q4_0_mfma_stream<XQ, kStreamWaves, kStreamDepth, PW>;
+    const void* fn = (const void*)q4_0_mfma_stream<XQ, NW, D, PW>;
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
-    hipLaunchKernelGGL((q4_0_mfma_stream<XQ, kStreamWaves, kStreamDepth, PW>), dim3(grid), dim3(kStreamWaves * 64),
-                       lds, st, w, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate);
+    hipLaunchKernelGGL((q4_0_mfma_stream<XQ, NW, D, PW>), dim3(grid), dim3(NW * 64), lds, st, w, x, y, M, K, o.pre,
+                       o.pre_arg, o.eps, (int)o.accumulate);
     return kOk;
 }
 
-// Workgroup layout of one launch: grid size, tiles per workgroup, LDS bytes.
+// x items (8 positions) per thread -> the matching instantiation
+template <int NW, int D>
+int launch_nw(const uint8_t* w, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
+              const MatvecOpts& o) {
+    const int nb = K / 32;
+    const int xq = (nb * 4 + NW * 64 - 1) / (NW * 64);
+    if (xq <= 1) return launch_xq<1, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);
+    if (xq <= 2) return launch_xq<2, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);
+    return launch_xq<4, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);  // nb <= 512, NW >= 8: at most 4 items per thread
+}
+
+// Workgroup layout of one launch: grid size, tiles per workgroup, waves, LDS bytes.
 struct StreamShape {
-    int grid, tiles_per_group;
+    int grid, tiles_per_group, waves;
     size_t lds;
 };
 
 int compute_units();
+
+size_t stream_lds(int nw, int nb, int tiles_per_group) {
+    return (size_t)nw * kSlotBytes + (size_t)nb * (kXStride + 4) + (size_t)tiles_per_group * nw * 16 * sizeof(float);
+}
 
 StreamShape stream_shape(int64_t M, int64_t K) {
     const int nb = (int)(K / 32);
@@ -413,8 +436,12 @@ StreamShape stream_shape(int64_t M, int64_t K) {
     StreamShape sh;
     sh.grid = std::max(std::min(n_tiles, compute_units()), (n_tiles + kMaxTilesPerGroup - 1) / kMaxTilesPerGroup);
     sh.tiles_per_group = (n_tiles + sh.grid - 1) / sh.grid;
-    sh.lds = (size_t)kStreamWaves * kSlotBytes + (size_t)nb * (kXStride + 4) +
-             (size_t)sh.tiles_per_group * kStreamWaves * 16 * sizeof(float);
+    sh.waves = kWideWaves;
+    sh.lds = stream_lds(kWideWaves, nb, sh.tiles_per_group);
+    if (sh.lds > kLdsBudget) {
+        sh.waves = kNarrowWaves;
+        sh.lds = stream_lds(kNarrowWaves, nb, sh.tiles_per_group);
+    }
     return sh;
 }
 
@@ -443,28 +470,23 @@ bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& o, int6
     return K % 256 == 0 && nb >= kUnitBlocks && nb <= kMaxBlocks && M >= 1 && M <= INT32_MAX - 16 &&
            (M + 16) * nb * 18 < (int64_t)kPastEnd && (uintptr_t)w % 4 == 0 && (uintptr_t)x % 16 == 0 &&
            (o.pre == kPreNone || (uintptr_t)o.pre_arg % 16 == 0) &&
-           stream_shape(M, K).lds + 256 <= 160 * 1024;
+           stream_shape(M, K).lds <= kLdsBudget;
 }
 
 int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st,
                      const MatvecOpts& o) {
     const int nb = (int)(K / 32);
     const StreamShape sh = stream_shape(M, K);
-    const int grid = sh.grid;
-    const size_t lds = sh.lds;
-    const int xq = (nb * 4 + kStreamWaves * 64 - 1) / (kStreamWaves * 64);  // x items (8 positions) per thread
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const int m = (int)M, k = (int)K;
     int rc;
-    const int nu = nb / kUnitBlocks;  // units per tile
-    if (nu == kStreamWaves * 2)  // K = 4096: two units per wave and tile, x operands in registers
-        rc = launch_xq<1, 2>(wb, x, y, m, k, grid, lds, st, o);
-    else if (xq <= 1)
-        rc = launch_xq<1, 0>(wb, x, y, m, k, grid, lds, st, o);
-    else if (xq <= 2)
-        rc = launch_xq<2, 0>(wb, x, y, m, k, grid, lds, st, o);
+    if (sh.waves == kWideWaves && nb / kUnitBlocks == kWideWaves)
+        // K = 4096: one unit per wave and tile, the wave's x operands in registers
+        rc = launch_xq<1, kWideWaves, kWideDepth, 1>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
+    else if (sh.waves == kWideWaves)
+        rc = launch_nw<kWideWaves, kWideDepth>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
     else
-        rc = launch_xq<4, 0>(wb, x, y, m, k, grid, lds, st, o);  // nb <= 512: at most 4 items per thread
+        rc = launch_nw<kNarrowWaves, kNarrowDepth>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
     if (rc) return rc;
     ASMHIP_TRY(hipGetLastError());
     return kOk;
