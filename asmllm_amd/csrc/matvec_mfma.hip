@@ -315,7 +315,7 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
     const uint8_t* rowp = rowd + 4 * g;              // this lane's qs dword
     float acc = 0.f;
     if constexpr (PW > 0) {
-        static_assert(PW % D == 0, "a tile's units fill whole rounds of the load ring");
+        static_assert(D % PW == 0 || PW % D == 0, "the load ring and the tile's units align");
         long aq[PW][kUnitBlocks];
         float xsr[PW][kUnitBlocks];
 #pragma unroll
@@ -326,10 +326,13 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
                 aq[j][b] = *reinterpret_cast<const long*>(xdig + blk * kXStride + aoff);
                 xsr[j][b] = xscale[blk];
             }
-        for (int i = 0; i < my_tiles; ++i) {
+        // whole rounds of max(D, PW) units: units past the stream's end were
+        // loaded as zeros and only their partial-sum writes are skipped
+        constexpr int R = D > PW ? D : PW;
+        for (int s0 = 0; s0 < L; s0 += R) {
 #pragma unroll
-            for (int j = 0; j < PW; ++j) {
-                const int d = j % D, s = i * PW + j;
+            for (int r = 0; r < R; ++r) {
+                const int s = s0 + r, j = r % PW, d = r % D;
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
                     const int q = lane + 64 * k;
@@ -339,10 +342,12 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
                 acc = chunk_dot_x<kUnitBlocks>(rowd, rowp, aq[j], xsr[j], acc);
                 __builtin_amdgcn_wave_barrier();
                 load_unit(buf[d], s + D);
+                if (j == PW - 1) {  // last unit of tile s / PW
+                    const float acc2 = __shfl_down(acc, 16, 64);  // level 2 of row n
+                    if (g == 0 && s < L) part[((s / PW) * NW + wave) * 16 + n] = fmaf(acc2, 9.313225746154785e-10f, acc);  // 2^-30
+                    acc = 0.f;
+                }
             }
-            const float acc2 = __shfl_down(acc, 16, 64);  // level 2 of row n
-            if (g == 0) part[(i * NW + wave) * 16 + n] = fmaf(acc2, 9.313225746154785e-10f, acc);  // 2^-30
-            acc = 0.f;
         }
     } else
     for (int s0 = 0; s0 < L; s0 += D) {
