@@ -391,11 +391,23 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
     __shared__ int bi[16];
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float x = logits[i];
-        if (x > v) {
-            v = x;
-            idx = i;
+    // 8 elements per thread and pass, all loaded before any is compared (one
+    // memory round per 8192 logits instead of one per 1024); within a thread
+    // indices rise, so strict > keeps the first maximum
+    for (int base = 0; base < n; base += 8 * 1024) {
+        float x[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = base + k * 1024 + (int)threadIdx.x;
+            x[k] = i < n ? logits[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = base + k * 1024 + (int)threadIdx.x;
+            if (x[k] > v) {
+                v = x[k];
+                idx = i;
+            }
         }
     }
 #pragma unroll

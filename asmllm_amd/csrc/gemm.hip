@@ -205,14 +205,14 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_kernel(const uint8_t* __r
 // operand read land in distinct banks).  Operands are realigned as they are
 // read: qs of an even block start 2 bytes past a dword.
 // ---------------------------------------------------------------------------
-template <int KB>
+template <int KB, int NTH>
 struct RawStep {
     static constexpr int kChunk = KB * 34;                        // bytes of a row's K chunk
     static constexpr int kPieces = (kChunk + 15) / 16;            // 16-byte loads per row
     static constexpr int kPitch = ((kPieces * 16 / 4) | 1) * 4;   // odd number of dwords
     static constexpr int kRows = kTT + kTM;
     static constexpr int kTotal = kRows * kPieces;
-    static constexpr int kPerThread = (kTotal + kThreadsG - 1) / kThreadsG;
+    static constexpr int kPerThread = (kTotal + NTH - 1) / NTH;
     static constexpr int kStage = kRows * kPitch + 16;             // + spare dwords for dead slots
 };
 
@@ -242,12 +242,16 @@ __device__ __forceinline__ v4h raw_scale(const uint8_t* row) {
     return v;
 }
 
-template <int KB, int D>
-__global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* __restrict__ w,
-                                                                 const uint8_t* __restrict__ a,
-                                                                 float* __restrict__ c, int T, int M, int K,
-                                                                 int tiles_t, int n_tiles) {
-    using S = RawStep<KB>;
+// WT = 32-column tiles per wave: 2 -> 4 waves of 32x64 (256 threads),
+// 1 -> 8 waves of 32x32 (512 threads, twice the waves to hide each wave's
+// MFMA -> epilogue latency).
+template <int KB, int D, int WT>
+__global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* __restrict__ w,
+                                                               const uint8_t* __restrict__ a,
+                                                               float* __restrict__ c, int T, int M, int K,
+                                                               int tiles_t, int n_tiles) {
+    constexpr int NTH = 512 / WT, MW = 4 / WT;  // threads; waves along M
+    using S = RawStep<KB, NTH>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     // XCD-aware tile order: workgroup ids are dealt round-robin to the 8 XCDs,
     // so id -> (xcd = id % 8, j = id / 8) -> tile xcd * chunk + j gives each XCD
@@ -261,7 +265,7 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* 
     const int t0 = (tile % tiles_t) * kTT, j0 = (tile / tiles_t) * kTM;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wt = wave >> 1, wm = wave & 1;
+    const int wt = wave / MW, wm = wave % MW;
     const auto ar = make_rsrc(a, row_bytes * (uint32_t)T);
     const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
 
@@ -272,7 +276,7 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* 
     bool is_a[S::kPerThread];
 #pragma unroll
     for (int i = 0; i < S::kPerThread; ++i) {
-        const int q = (int)threadIdx.x + kThreadsG * i;
+        const int q = (int)threadIdx.x + NTH * i;
         const bool live = q < S::kTotal;
         const int qq = live ? q : 0;
         const int r = qq / S::kPieces, k = qq - r * S::kPieces;
@@ -302,9 +306,9 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* 
     };
 
     const int m = lane & 31, g = lane >> 5;
-    v16f acc[2];
+    v16f acc[WT];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < WT; ++nt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[nt][i] = 0.f;
 
@@ -322,30 +326,29 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* 
             __syncthreads();
             if (s + D < nsteps) fetch(pre[u], (s + D) * KB);
             const uint8_t* arow = stage + (32 * wt + m) * S::kPitch;
-            const uint8_t* wrow0 = stage + (kTT + 64 * wm + m) * S::kPitch;
-            const uint8_t* wrow1 = wrow0 + 32 * S::kPitch;
+            const uint8_t* wrow = stage + (kTT + 32 * WT * wm + m) * S::kPitch;
             // block BLK (0 or 1) of the dword-aligned pair at byte 68 bp
             auto block = [&](auto blk_c, int bp) {
                 constexpr int BLK = decltype(blk_c)::value;
                 const uint8_t* ar_ = arow + 68 * bp;
-                const uint8_t* w0_ = wrow0 + 68 * bp;
-                const uint8_t* w1_ = wrow1 + 68 * bp;
                 const v4i av = raw_qs<BLK>(ar_, g);
                 const v4h da = raw_scale<BLK>(ar_);
-                const v4i bv0 = raw_qs<BLK>(w0_, g);
-                const v4h dw0 = raw_scale<BLK>(w0_);
-                const v4i bv1 = raw_qs<BLK>(w1_, g);
-                const v4h dw1 = raw_scale<BLK>(w1_);
                 const v16i zi = {};
                 const v16f zf = {};
-                const v16i d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv0, zi, 0, 0, 0);
-                const v16f s0 = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw0, zf, 0, 0, 0);  // 2 d_a d_w
-                const v16i d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv1, zi, 0, 0, 0);
-                const v16f s1 = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw1, zf, 0, 0, 0);
+                v16i dd[WT];
+                v16f ss[WT];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[0][i] = fmaf((float)d0[i], s0[i], acc[0][i]);
+                for (int nt = 0; nt < WT; ++nt) {
+                    const uint8_t* w_ = wrow + 32 * nt * S::kPitch + 68 * bp;
+                    const v4i bv = raw_qs<BLK>(w_, g);
+                    const v4h dw = raw_scale<BLK>(w_);
+                    dd[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zi, 0, 0, 0);
+                    ss[nt] = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw, zf, 0, 0, 0);  // 2 d_a d_w
+                }
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[1][i] = fmaf((float)d1[i], s1[i], acc[1][i]);
+                for (int nt = 0; nt < WT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) acc[nt][i] = fmaf((float)dd[nt][i], ss[nt][i], acc[nt][i]);
             };
 #pragma unroll 1
             for (int bp = 0; bp < KB / 2; ++bp) {
@@ -356,8 +359,8 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* 
     }
 
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int col = j0 + 64 * wm + 32 * nt + m;
+    for (int nt = 0; nt < WT; ++nt) {
+        const int col = j0 + 32 * WT * wm + 32 * nt + m;
         if (col >= M) continue;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -369,9 +372,10 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_coalesced(const uint8_t* 
 
 // Two blocks per staged K step, one step of loads in flight per thread.
 // Deeper register rings (2-4 steps) and 4- or 8-block steps measured slower on
-// MI355X: the extra registers cost occupancy, which this VALU-bound loop needs.
+// MI355X: the extra registers cost occupancy.
 constexpr int kGemmKB = 2;  // blocks per staged K step (even)
 constexpr int kGemmD = 1;   // K steps of loads in flight per thread
+constexpr int kGemmWT = 2;  // 32-column tiles per wave (8 waves of one tile measured 6% slower)
 
 }  // namespace
 
@@ -388,10 +392,11 @@ int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t 
     if ((K / 32) % kGemmKB == 0) {
         const int tiles_t = (int)grid.y, n_tiles = (int)(grid.x * grid.y);
         const unsigned padded = (unsigned)((n_tiles + 7) / 8 * 8);
-        const size_t lds = 2 * (size_t)RawStep<kGemmKB>::kStage;
-        const int rc = dynamic_lds((const void*)gemm_q8_0_coalesced<kGemmKB, kGemmD>, lds);
+        constexpr int kThreads = 512 / kGemmWT;
+        const size_t lds = 2 * (size_t)RawStep<kGemmKB, kThreads>::kStage;
+        const int rc = dynamic_lds((const void*)gemm_q8_0_coalesced<kGemmKB, kGemmD, kGemmWT>, lds);
         if (rc) return rc;
-        hipLaunchKernelGGL((gemm_q8_0_coalesced<kGemmKB, kGemmD>), dim3(padded), dim3(kThreadsG), lds, st,
+        hipLaunchKernelGGL((gemm_q8_0_coalesced<kGemmKB, kGemmD, kGemmWT>), dim3(padded), dim3(kThreads), lds, st,
                            static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(a), c, (int)T, (int)M, (int)K,
                            tiles_t, n_tiles);
     } else {
