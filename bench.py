@@ -589,7 +589,7 @@ def main() -> None:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": round(traffic["bytes"]) if traffic else None,
             "traffic_detail": traffic,
-            "kernel": "q4_0_mfma_stream (int8 MFMA, GGUF Q4_0)",
+            "kernel": "q4_0_mfma_stream<1,16,1,1> (int8 MFMA, GGUF Q4_0)",
             "kernel_us_mean": round(mv["kernel_us_mean"], 3),
             "fp32_valu_kernel_us_mean": round(mv["fp32_kernel_us_mean"], 3),
             "bytes_per_launch": mv["bytes_per_step"],
