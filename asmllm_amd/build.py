@@ -86,10 +86,17 @@ def build_library(jobs: int | None = None) -> Path:
     return LIB_PATH
 
 
+REFERENCE = Path("/root/reference")
+
+
 def build_oracle() -> Path:
-    """Compiles the CPU oracle (test infrastructure) with its Makefile."""
+    """Compiles the CPU oracle (test infrastructure) with its Makefile, and,
+    where the reference tree is present, the reference's own GGUF loader into
+    oracle/_ref/ (the checker of the GGUF reader)."""
     oracle_dir = REPO / "oracle"
     _run(["make", "-s", "-C", str(oracle_dir), "-B", "liboracle.so"])
+    if (REFERENCE / "src" / "loader" / "gguf_loader.c").exists():
+        _run(["make", "-s", "-C", str(oracle_dir), "-B", f"REF={REFERENCE}", "_ref/libgguf_ref.so"])
     return oracle_dir / "liboracle.so"
 
 

@@ -81,6 +81,29 @@ class LlamaShape:
 LLAMA_7B = LlamaShape()
 
 
+def shape_from_gguf(g) -> LlamaShape:
+    """LlamaShape from a GGUFFile's llama.* metadata (the fields generate.py:123-141
+    fixes for its model); the vocabulary size from the token embedding."""
+    md = g.metadata
+    arch = md.get("general.architecture", "llama")
+
+    def get(key, default=None):
+        v = md.get(f"{arch}.{key}", default)
+        if v is None:
+            raise ValueError(f"{g.path}: metadata {arch}.{key} missing")
+        return v
+
+    n_heads = int(get("attention.head_count"))
+    emb = g.tensors.get("token_embd.weight")
+    if emb is None:
+        raise ValueError(f"{g.path}: no token_embd.weight")
+    return LlamaShape(dim=int(get("embedding_length")), n_layers=int(get("block_count")), n_heads=n_heads,
+                      n_kv_heads=int(get("attention.head_count_kv", n_heads)),
+                      hidden_dim=int(get("feed_forward_length")), vocab=int(emb.dims[1]),
+                      eps=float(get("attention.layer_norm_rms_epsilon", 1e-5)),
+                      theta=float(get("rope.freq_base", 10000.0)))
+
+
 class _Layer:
     def __init__(self, s: LlamaShape, max_ctx: int):
         d, h = s.dim, s.hidden_dim
@@ -129,6 +152,7 @@ class DecodeEngine:
         self.workspace = DeviceBuffer(4 * max(int(ws), 1))
         self.token = DeviceBuffer(4)
         self.pos = DeviceBuffer(4)
+        self.vocab: list[str] = []
         self._graph: Graph | None = None
 
     # ---- model data ---------------------------------------------------------------
@@ -172,6 +196,48 @@ class DecodeEngine:
         self.embed.upload(embed)
         self.final_norm.upload(np.asarray(final_norm, np.float32))
         self.output.upload(output)
+
+    @classmethod
+    def from_gguf(cls, path, max_ctx: int = 2048, stream: Stream | None = None) -> "DecodeEngine":
+        """Engine for a Llama GGUF model, every tensor uploaded once to HBM
+        (the tensor names of generate.py:182-205; the shape from the llama.*
+        metadata).  Linear weights and the token embedding must be Q4_0, norm
+        weights F32; a model without output.weight uses the token embedding
+        as its lm-head."""
+        from .gguf_file import F32, Q4_0, GGUFFile
+
+        g = GGUFFile(path)
+        try:
+            shape = shape_from_gguf(g)
+            eng = cls(shape, max_ctx=max_ctx, stream=stream)
+
+            def q4(name):
+                t = g.tensors.get(name)
+                if t is None:
+                    raise KeyError(f"{path}: no tensor {name!r}")
+                if t.type != Q4_0:
+                    raise ValueError(f"{name}: tensor type {t.type}; the engine takes Q4_0 ({Q4_0}) weights")
+                return g.tensor(name)
+
+            def f32(name):
+                t = g.tensors.get(name)
+                if t is None or t.type != F32:
+                    raise ValueError(f"{name}: missing or not F32")
+                return g.tensor(name)
+
+            for i in range(shape.n_layers):
+                b = f"blk.{i}."
+                eng.load_layer(i, attn_norm=f32(b + "attn_norm.weight"), wq=q4(b + "attn_q.weight"),
+                               wk=q4(b + "attn_k.weight"), wv=q4(b + "attn_v.weight"), wo=q4(b + "attn_output.weight"),
+                               ffn_norm=f32(b + "ffn_norm.weight"), w_gate=q4(b + "ffn_gate.weight"),
+                               w_up=q4(b + "ffn_up.weight"), w_down=q4(b + "ffn_down.weight"))
+            embed = q4("token_embd.weight")
+            output = q4("output.weight") if "output.weight" in g.tensors else embed
+            eng.load_globals(embed=embed, final_norm=f32("output_norm.weight"), output=output)
+            eng.vocab = g.vocab()
+        finally:
+            g.close()
+        return eng
 
     def load_kv(self, i: int, k_cache: np.ndarray, v_cache: np.ndarray) -> None:
         """fp16 caches of layer i as [n_kv_heads][max_ctx][head_dim] (uint16 bits or float16)."""

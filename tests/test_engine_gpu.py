@@ -124,3 +124,71 @@ def test_7b_shape_step_at_context_2048_matches_oracle():
     rel = _check_logits(got, want, "7B step")
     print(f"7B step: max err / max|logit| {rel:.2e}")
     eng.close()
+
+
+def _write_llama_gguf(path, s: LlamaShape, seed: int, tied: bool):
+    from asmllm_amd import gguf
+    from asmllm_amd import gguf_file as gf
+
+    rng = np.random.default_rng(seed)
+
+    def q4(rows, K):
+        return gguf.quantize_q4_0((rng.standard_normal((rows, K)) * 0.05).astype(np.float32))
+
+    d, h, kv = s.dim, s.hidden_dim, s.kv_dim
+    t = {"token_embd.weight": (gf.Q4_0, (d, s.vocab), q4(s.vocab, d)),
+         "output_norm.weight": (gf.F32, (d,), rng.uniform(0.5, 1.5, d).astype(np.float32))}
+    if not tied:
+        t["output.weight"] = (gf.Q4_0, (d, s.vocab), q4(s.vocab, d))
+    for i in range(s.n_layers):
+        b = f"blk.{i}."
+        t[b + "attn_norm.weight"] = (gf.F32, (d,), rng.uniform(0.5, 1.5, d).astype(np.float32))
+        t[b + "ffn_norm.weight"] = (gf.F32, (d,), rng.uniform(0.5, 1.5, d).astype(np.float32))
+        for name, rows, K in (("attn_q", d, d), ("attn_k", kv, d), ("attn_v", kv, d), ("attn_output", d, d),
+                              ("ffn_gate", h, d), ("ffn_up", h, d), ("ffn_down", d, h)):
+            t[b + name + ".weight"] = (gf.Q4_0, (K, rows), q4(rows, K))
+    meta = {"general.architecture": (gf.T_STRING, "llama"),
+            "llama.embedding_length": (gf.T_UINT32, d), "llama.block_count": (gf.T_UINT32, s.n_layers),
+            "llama.feed_forward_length": (gf.T_UINT32, h), "llama.attention.head_count": (gf.T_UINT32, s.n_heads),
+            "llama.attention.head_count_kv": (gf.T_UINT32, s.n_kv_heads),
+            "llama.attention.layer_norm_rms_epsilon": (gf.T_FLOAT32, s.eps),
+            "llama.rope.freq_base": (gf.T_FLOAT32, s.theta),
+            "tokenizer.ggml.tokens": (gf.T_ARRAY, (gf.T_STRING, [f"t{i}" for i in range(s.vocab)]))}
+    gf.write_gguf(path, meta, t, alignment=64)
+
+
+@pytest.mark.parametrize("tied", [False, True], ids=["lm_head", "tied_embedding"])
+def test_engine_from_gguf_matches_oracle(tmp_path, tied):
+    """A GGUF Llama (generate.py:182-205 tensor names) loaded once into HBM
+    decodes as the oracle's forward_token on the file's own tensors."""
+    from asmllm_amd import gguf_file as gf
+    from oracle.decode_ref import DecodeRef
+
+    s = LlamaShape(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, hidden_dim=512, vocab=500,
+                   eps=float(np.float32(1e-5)))  # as the file stores it
+    path = tmp_path / "tiny.gguf"
+    _write_llama_gguf(path, s, seed=11, tied=tied)
+    max_ctx = 32
+    eng = DecodeEngine.from_gguf(path, max_ctx=max_ctx)
+    assert eng.shape == s and eng.vocab[:2] == ["t0", "t1"]
+    with gf.GGUFFile(path) as g:
+        T = lambda n: np.array(g.tensor(n))
+        layers = [{"attn_norm": T(f"blk.{i}.attn_norm.weight"), "ffn_norm": T(f"blk.{i}.ffn_norm.weight"),
+                   "wq": T(f"blk.{i}.attn_q.weight"), "wk": T(f"blk.{i}.attn_k.weight"),
+                   "wv": T(f"blk.{i}.attn_v.weight"), "wo": T(f"blk.{i}.attn_output.weight"),
+                   "w_gate": T(f"blk.{i}.ffn_gate.weight"), "w_up": T(f"blk.{i}.ffn_up.weight"),
+                   "w_down": T(f"blk.{i}.ffn_down.weight")} for i in range(s.n_layers)]
+        embed = T("token_embd.weight")
+        ref = DecodeRef(dim=s.dim, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, hidden_dim=s.hidden_dim,
+                        vocab=s.vocab, eps=s.eps, theta=s.theta, embed=embed,
+                        final_norm=T("output_norm.weight"), output=embed if tied else T("output.weight"),
+                        layers=layers,
+                        k_caches=[np.zeros((s.n_kv_heads, max_ctx, s.head_dim), np.uint16)] * s.n_layers,
+                        v_caches=[np.zeros((s.n_kv_heads, max_ctx, s.head_dim), np.uint16)] * s.n_layers)
+    token = 1
+    for pos in range(6):  # from position 0: every cache row read was written by an earlier step
+        got = eng.forward_token(token, pos)
+        want = ref.forward_token(token, pos)
+        _check_logits(got, want, f"pos {pos}")
+        token = int(np.argmax(want))
+    eng.close()
