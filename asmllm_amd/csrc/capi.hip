@@ -218,6 +218,26 @@ int sync_matvec(QuantType qt, const void* q, const float* s, const float* x, flo
     });
 }
 
+int sync_matvec_q5(const uint8_t* ql, const uint8_t* qh, const float* s, const float* x, float* y, int64_t M,
+                   int64_t K) {
+    if (M <= 0 || K <= 0 || K % 32 != 0)
+        return fail(kInvalidArgument, "need M > 0, K > 0 and K %% 32 == 0 (got M=%lld K=%lld)", (long long)M,
+                    (long long)K);
+    const size_t nb = (size_t)(K / 32);
+    Operand ops[5] = {
+        {ql, (size_t)M * nb * 16, true, false},
+        {qh, (size_t)M * nb * 4, true, false},
+        {s, (size_t)M * nb * sizeof(float), true, false},
+        {x, (size_t)K * sizeof(float), true, false},
+        {y, (size_t)M * sizeof(float), false, true},
+    };
+    return sync_call(ops, 5, [&](hipStream_t stream) {
+        return q5_matvec_launch(false, ops[0].dev, static_cast<const uint8_t*>(ops[1].dev),
+                                static_cast<const float*>(ops[2].dev), static_cast<const float*>(ops[3].dev),
+                                static_cast<float*>(ops[4].dev), M, K, stream);
+    });
+}
+
 void record_pool_size(int n) {
     if (n < 1) n = 1;
     if (n > kMaxPool) n = kMaxPool;
@@ -244,6 +264,11 @@ extern "C" void asm_matmul_q4_avx512(const uint8_t* qweights, const float* scale
 extern "C" void asm_matmul_q8(const int8_t* qweights, const float* scales, const float* x, float* y, int64_t M,
                               int64_t K) {
     report(sync_matvec(QuantType::Q8_0, qweights, scales, x, y, M, K), "asm_matmul_q8");
+}
+
+extern "C" void asm_matmul_q5(const uint8_t* ql, const uint8_t* qh, const float* scales, const float* x, float* y,
+                              int64_t M, int64_t K) {
+    report(sync_matvec_q5(ql, qh, scales, x, y, M, K), "asm_matmul_q5");
 }
 
 extern "C" void asm_threadpool_init(int num_threads) {
@@ -309,6 +334,17 @@ extern "C" void asm_matmul_q8_mt(const int8_t* qweights, const float* scales, co
 extern "C" void asm_threadpool_dispatch_q8(const int8_t* qweights, const float* scales, const float* x, float* y,
                                            int64_t M, int64_t K) {
     report(sync_matvec(QuantType::Q8_0, qweights, scales, x, y, M, K), "asm_threadpool_dispatch_q8");
+}
+
+extern "C" void asm_matmul_q5_mt(const uint8_t* ql, const uint8_t* qh, const float* scales, const float* x, float* y,
+                                 int64_t M, int64_t K, int num_threads) {
+    mt_pool_update(M, num_threads);
+    report(sync_matvec_q5(ql, qh, scales, x, y, M, K), "asm_matmul_q5_mt");
+}
+
+extern "C" void asm_threadpool_dispatch_q5(const uint8_t* ql, const uint8_t* qh, const float* scales, const float* x,
+                                           float* y, int64_t M, int64_t K) {
+    report(sync_matvec_q5(ql, qh, scales, x, y, M, K), "asm_threadpool_dispatch_q5");
 }
 
 // rmsnorm_avx2.asm:63-151: y = (x * (1/sqrt(mean(x^2) + eps))) * w.
@@ -414,6 +450,23 @@ extern "C" int asmhip_matmul_q8_split(const int8_t* qweights, const float* scale
     int rc = check_ptrs(qweights, x, y);
     if (!rc && !scales) rc = fail(kInvalidArgument, "null scales");
     return rc ? rc : matvec_launch(QuantType::Q8_0, false, qweights, scales, x, y, M, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_matmul_q5_split(const uint8_t* ql, const uint8_t* qh, const float* scales, const float* x,
+                                      float* y, int64_t M, int64_t K, void* stream) {
+    int rc = check_ptrs(ql, x, y);
+    if (!rc && (!qh || !scales)) rc = fail(kInvalidArgument, "null qh or scales");
+    return rc ? rc : q5_matvec_launch(false, ql, qh, scales, x, y, M, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_matmul_q5_0(const void* blocks, const float* x, float* y, int64_t M, int64_t K, void* stream) {
+    int rc = check_ptrs(blocks, x, y);
+    return rc ? rc : q5_matvec_launch(true, blocks, nullptr, nullptr, x, y, M, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_dequantize_q5_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream) {
+    if (!blocks || !w) return fail(kInvalidArgument, "null pointer argument");
+    return q5_dequant_launch(blocks, w, rows, K, (hipStream_t)stream);
 }
 
 extern "C" int asmhip_dequantize_q4_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream) {

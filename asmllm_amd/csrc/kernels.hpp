@@ -30,6 +30,13 @@ struct MatvecOpts {
 int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, const float* x, float* y,
                   int64_t M, int64_t K, hipStream_t stream, const MatvecOpts& opts = MatvecOpts());
 
+// Q5_0 y = W x.  gguf: W is [M][K/32] 22-byte GGUF blocks (qh, scales unused);
+// otherwise the split layout: ql = w [M][K/32][16], qh [M][K/32][4] and fp32
+// scales [M][K/32].
+int q5_matvec_launch(bool gguf, const void* w, const uint8_t* qh, const float* scales, const float* x, float* y,
+                     int64_t M, int64_t K, hipStream_t stream);
+int q5_dequant_launch(const void* blocks, float* out, int64_t rows, int64_t K, hipStream_t stream);
+
 // Q4_0 GGUF matvec on the int8 matrix cores (matvec_launch picks it when
 // q4_0_mfma_eligible holds: K % 256 == 0, K <= 16384, 16-byte aligned x).
 // Process-wide choice of the Q4_0 GGUF kernel: auto (MFMA when eligible), the

@@ -1,4 +1,4 @@
-// Q4_0 / Q8_0 matrix-vector kernels for gfx950.
+// Q4_0 / Q8_0 / Q5_0 matrix-vector kernels for gfx950 (VALU, fp32 accumulation).
 //
 // y[m] = sum_b d[m,b] * sum_j (q[m,b,j] - z) * x[32b + j],  z = 8 for Q4_0 and 0 for Q8_0
 //
@@ -368,6 +368,211 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t* __rest
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q5_0: b = nibble | (fifth bit << 4), weight (b - 16) * d
+// (src/kernels/x86_64/matmul_q5_avx2.asm:93-210, tests/reference/ops.py:67-92).
+// ql byte j holds weight j (low nibble) and weight j + 16 (high nibble); bit j
+// of the block's little-endian 32-bit qh word is weight j's fifth bit.
+//
+// Each weight becomes an exact float with one sign-extending byte conversion:
+// the byte ((b ^ 16) << 3), i.e. the nibble in bits 3..6 and the inverted
+// fifth bit in bit 7, reads as the signed value 8 (b - 16).  x is staged as
+// x / 8 (exact), so each product 8 (b - 16) * (x / 8) is exactly (b - 16) * x.
+// ---------------------------------------------------------------------------
+
+// Bits [4g, 4g + 4) of h at bit 7 of bytes 0..3 (the other bits are junk):
+// with t = those bits at [7, 11), t * (1 + 2^7 + 2^14 + 2^21) puts bit j of t
+// at 8j + 7; the four shifted copies of t do not overlap, so nothing carries,
+// and both factors fit the 24-bit multiplier.
+__device__ __forceinline__ uint32_t q5_high_bits(uint32_t h, int g) {
+    const int s = 4 * g - 7;
+    const uint32_t t = (s >= 0 ? (h >> s) : (h << -s)) & 0x780u;
+    return __umul24(t, 0x204081u);
+}
+
+// One block: q = its four ql words, nh = ~qh word, xb = x / 8 of its 32 columns.
+__device__ __forceinline__ float q5_block(const uint32_t* q, uint32_t nh, const float* xb) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = opaque(((q[i] << 3) & 0x78787878u) | (q5_high_bits(nh, i) & 0x80808080u));
+        const uint32_t hi = opaque(((q[i] >> 1) & 0x78787878u) | (q5_high_bits(nh, 4 + i) & 0x80808080u));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            t = fmaf(sbyte(lo, k), xb[4 * i + k], t);
+            t = fmaf(sbyte(hi, k), xb[16 + 4 * i + k], t);
+        }
+    }
+    return t;
+}
+
+// Q5_0 pair kernel (the mapping of the Q4_0 one).  kGguf: 22-byte blocks
+// (fp16 d, qh[4], qs[16]); a pair is 44 bytes, so with K/32 even every pair
+// starts on a dword and block A's fields sit two bytes off the dword grid.
+// Otherwise the split layout: w = ql, wh = qh, wscale = fp32 scales.
+template <int R, bool kGguf>
+__global__ __launch_bounds__(kThreads) void q5_matvec_pairs(const uint8_t* __restrict__ w,
+                                                            const uint8_t* __restrict__ wh,
+                                                            const float* __restrict__ wscale,
+                                                            const float* __restrict__ x,
+                                                            float* __restrict__ y, int M, int K) {
+    extern __shared__ float xs[];
+    stage_x(x, xs, K, 0.125f, kPreNone, nullptr, 0.f);
+
+    const int nb = K >> 5;
+    const int np = nb >> 1;
+    const uint32_t row_bytes = kGguf ? (uint32_t)nb * 22u : (uint32_t)nb * 16u;
+    const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
+    const auto hr = make_rsrc(wh, kGguf ? 0u : (uint32_t)nb * 4u * (uint32_t)M);
+    const auto sr = make_rsrc(wscale, kGguf ? 0u : (uint32_t)nb * 4u * (uint32_t)M);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nwaves = gridDim.x * kWavesPerBlock;
+
+    for (int g = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6); g * R < M; g += nwaves) {
+        const int row0 = g * R;
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+
+        for (int c0 = 0; c0 < np; c0 += kWave) {
+            const int p = c0 + lane;
+            const bool active = p < np;
+            const int pc = active ? p : np - 1;
+
+            uint32_t v[R][11];
+            float dA[R], dB[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = min(row0 + r, M - 1);
+                if (kGguf) {
+                    const uint32_t off = (uint32_t)row * row_bytes + (uint32_t)pc * 44u;
+                    const uint4 a = buf_load_b128(wr, off);
+                    const uint4 b = buf_load_b128(wr, off + 16u);
+                    const uint2 c = buf_load_b64(wr, off + 32u);
+                    v[r][0] = a.x; v[r][1] = a.y; v[r][2] = a.z; v[r][3] = a.w;
+                    v[r][4] = b.x; v[r][5] = b.y; v[r][6] = b.z; v[r][7] = b.w;
+                    v[r][8] = c.x; v[r][9] = c.y;
+                    v[r][10] = buf_load_b32(wr, off + 40u);
+                } else {
+                    const uint32_t blk = (uint32_t)row * (uint32_t)nb + 2u * (uint32_t)pc;
+                    const uint4 a = buf_load_b128(wr, blk * 16u);
+                    const uint4 b = buf_load_b128(wr, blk * 16u + 16u);
+                    const uint2 h = buf_load_b64(hr, blk * 4u);
+                    const uint2 sc = buf_load_b64(sr, blk * 4u);
+                    v[r][0] = a.x; v[r][1] = a.y; v[r][2] = a.z; v[r][3] = a.w;
+                    v[r][4] = b.x; v[r][5] = b.y; v[r][6] = b.z; v[r][7] = b.w;
+                    v[r][8] = h.x; v[r][9] = h.y;
+                    dA[r] = __uint_as_float(sc.x);
+                    dB[r] = __uint_as_float(sc.y);
+                }
+            }
+
+            float xr[64];
+            const float4* xq = reinterpret_cast<const float4*>(xs + xpad(pc * 64));
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const float4 t = xq[q];
+                xr[4 * q] = t.x; xr[4 * q + 1] = t.y; xr[4 * q + 2] = t.z; xr[4 * q + 3] = t.w;
+            }
+
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint32_t qa[4], qb[4], ha, hb;
+                if (kGguf) {
+                    // bytes: [0,2) dA, [2,6) qhA, [6,22) qsA, [22,24) dB, [24,28) qhB, [28,44) qsB
+                    dA[r] = half_lo(v[r][0]);
+                    dB[r] = half_hi(v[r][5]);
+                    ha = __builtin_amdgcn_alignbyte(v[r][1], v[r][0], 2);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) qa[i] = __builtin_amdgcn_alignbyte(v[r][i + 2], v[r][i + 1], 2);
+                    hb = v[r][6];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) qb[i] = v[r][7 + i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        qa[i] = v[r][i];
+                        qb[i] = v[r][4 + i];
+                    }
+                    ha = v[r][8];
+                    hb = v[r][9];
+                }
+                const float tA = q5_block(qa, ~ha, xr);
+                const float tB = q5_block(qb, ~hb, xr + 32);
+                float a = fmaf(dA[r], tA, acc[r]);
+                a = fmaf(dB[r], tB, a);
+                acc[r] = active ? a : acc[r];
+            }
+        }
+
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float s = wave_sum(acc[r]);
+            if (lane == r && row0 + r < M) y[row0 + r] = s;
+        }
+    }
+}
+
+// Generic Q5_0 kernel: one wave per row, one block per lane, byte loads (odd
+// K/32, unaligned operands, x too large for LDS).
+template <bool kGguf>
+__global__ __launch_bounds__(kThreads) void q5_matvec_generic(const uint8_t* __restrict__ w,
+                                                              const uint8_t* __restrict__ wh,
+                                                              const float* __restrict__ wscale,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y, int M, int K) {
+    const int nb = K >> 5;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    if (row >= M) return;
+    float acc = 0.f;
+    for (int b = lane; b < nb; b += kWave) {
+        const int64_t blk = (int64_t)row * nb + b;
+        const uint8_t* qs;
+        const uint8_t* qh;
+        float d;
+        if (kGguf) {
+            const uint8_t* p = w + blk * 22;
+            d = __half2float(__ushort_as_half((unsigned short)(p[0] | (p[1] << 8))));
+            qh = p + 2;
+            qs = p + 6;
+        } else {
+            d = wscale[blk];
+            qh = wh + blk * 4;
+            qs = w + blk * 16;
+        }
+        const uint32_t h = (uint32_t)qh[0] | ((uint32_t)qh[1] << 8) | ((uint32_t)qh[2] << 16) | ((uint32_t)qh[3] << 24);
+        const float* xb = x + (int64_t)b * 32;
+        float t = 0.f;
+        for (int j = 0; j < 16; ++j) {
+            const int lo = (qs[j] & 15) | (int)(((h >> j) & 1u) << 4);
+            const int hi = (qs[j] >> 4) | (int)(((h >> (j + 16)) & 1u) << 4);
+            t = fmaf((float)(lo - 16), xb[j], t);
+            t = fmaf((float)(hi - 16), xb[16 + j], t);
+        }
+        acc = fmaf(d, t, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
+// Exact dequantization of GGUF Q5_0 blocks: one thread per block.
+__global__ __launch_bounds__(kThreads) void q5_dequant_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
+                                                              int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint8_t* p = w + i * 22;
+    const float d = __half2float(__ushort_as_half((unsigned short)(p[0] | (p[1] << 8))));
+    const uint32_t h = (uint32_t)p[2] | ((uint32_t)p[3] << 8) | ((uint32_t)p[4] << 16) | ((uint32_t)p[5] << 24);
+    float* o = out + i * 32;
+    for (int j = 0; j < 16; ++j) {
+        const int lo = (p[6 + j] & 15) | (int)(((h >> j) & 1u) << 4);
+        const int hi = (p[6 + j] >> 4) | (int)(((h >> (j + 16)) & 1u) << 4);
+        o[j] = (float)(lo - 16) * d;
+        o[16 + j] = (float)(hi - 16) * d;
+    }
+}
+
 size_t pair_lds_bytes(int64_t K) { return (size_t)(K + K / 16) * sizeof(float); }
 
 int pick_rows_per_wave(int64_t M, int r_max) {
@@ -398,6 +603,17 @@ int launch_q8(const uint8_t* w, const float* s, const float* x, float* y, int M,
     const int blocks = (int)((groups + kWavesPerBlock - 1) / kWavesPerBlock);
     hipLaunchKernelGGL((q8_matvec_pairs<R, kGguf>), dim3(blocks), dim3(kThreads), lds, st, w, s, x, y, M, K, o.pre,
                        o.pre_arg, o.eps, (int)o.accumulate);
+    return kOk;
+}
+
+template <int R, bool kGguf>
+int launch_q5(const uint8_t* w, const uint8_t* h, const float* s, const float* x, float* y, int M, int K, size_t lds,
+              hipStream_t st) {
+    const int rc = dynamic_lds((const void*)q5_matvec_pairs<R, kGguf>, lds);
+    if (rc) return rc;
+    const int64_t groups = (M + R - 1) / R;
+    const int blocks = (int)((groups + kWavesPerBlock - 1) / kWavesPerBlock);
+    hipLaunchKernelGGL((q5_matvec_pairs<R, kGguf>), dim3(blocks), dim3(kThreads), lds, st, w, h, s, x, y, M, K);
     return kOk;
 }
 
@@ -509,6 +725,60 @@ int dequant_launch(QuantType qt, const void* w, float* out, int64_t rows, int64_
     else
         hipLaunchKernelGGL((dequant_kernel<true>), dim3((unsigned)grid), dim3(kThreads), 0, stream,
                            static_cast<const uint8_t*>(w), out, nblocks);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int q5_matvec_launch(bool gguf, const void* w, const uint8_t* qh, const float* scales, const float* x, float* y,
+                     int64_t M, int64_t K, hipStream_t stream) {
+    if (M <= 0 || K <= 0 || (K % 32) != 0)
+        return fail(kInvalidArgument, "matvec_q5: need M > 0, K > 0 and K %% 32 == 0 (got M=%lld K=%lld)",
+                    (long long)M, (long long)K);
+    if (M > INT32_MAX || K > INT32_MAX) return fail(kInvalidArgument, "matvec_q5: M and K must fit in int32");
+    const int64_t nb = K / 32;
+    const int64_t total = M * nb * (gguf ? 22 : 16);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    const size_t lds = pair_lds_bytes(K);
+    const bool aligned = ((uintptr_t)w % 4 == 0) && ((uintptr_t)x % 4 == 0) &&
+                         (gguf || ((uintptr_t)qh % 8 == 0 && (uintptr_t)scales % 8 == 0));
+    const bool pairs = nb % 2 == 0 && aligned && lds <= 160 * 1024 - 256 && total < (int64_t)UINT32_MAX;
+    const int m = (int)M, k = (int)K;
+    int rc = kOk;
+    if (pairs) {
+        const int r = pick_rows_per_wave(M, 4);
+        if (gguf) {
+            switch (r) {
+                case 4: rc = launch_q5<4, true>(wb, qh, scales, x, y, m, k, lds, stream); break;
+                case 2: rc = launch_q5<2, true>(wb, qh, scales, x, y, m, k, lds, stream); break;
+                default: rc = launch_q5<1, true>(wb, qh, scales, x, y, m, k, lds, stream); break;
+            }
+        } else {
+            switch (r) {
+                case 4: rc = launch_q5<4, false>(wb, qh, scales, x, y, m, k, lds, stream); break;
+                case 2: rc = launch_q5<2, false>(wb, qh, scales, x, y, m, k, lds, stream); break;
+                default: rc = launch_q5<1, false>(wb, qh, scales, x, y, m, k, lds, stream); break;
+            }
+        }
+    } else {
+        const int blocks = (int)((M + kWavesPerBlock - 1) / kWavesPerBlock);
+        if (gguf)
+            hipLaunchKernelGGL((q5_matvec_generic<true>), dim3(blocks), dim3(kThreads), 0, stream, wb, qh, scales, x, y, m, k);
+        else
+            hipLaunchKernelGGL((q5_matvec_generic<false>), dim3(blocks), dim3(kThreads), 0, stream, wb, qh, scales, x, y, m, k);
+    }
+    if (rc) return rc;
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int q5_dequant_launch(const void* w, float* out, int64_t rows, int64_t K, hipStream_t stream) {
+    if (rows <= 0 || K <= 0 || (K % 32) != 0)
+        return fail(kInvalidArgument, "dequantize: need rows > 0, K > 0 and K %% 32 == 0");
+    const int64_t nblocks = rows * (K / 32);
+    const int64_t grid = (nblocks + kThreads - 1) / kThreads;
+    if (grid > INT32_MAX) return fail(kInvalidArgument, "dequantize: tensor too large");
+    hipLaunchKernelGGL(q5_dequant_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream,
+                       static_cast<const uint8_t*>(w), out, nblocks);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

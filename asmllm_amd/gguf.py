@@ -1,9 +1,13 @@
-"""GGUF Q4_0 / Q8_0 block layouts on the host (numpy).
+"""GGUF Q4_0 / Q8_0 / Q5_0 block layouts on the host (numpy).
 
 Block layouts (32 weights per block):
   * Q4_0, 18 bytes: fp16 d, then 16 bytes; byte j holds weight j in its low
     nibble and weight j+16 in its high nibble; value = (nibble - 8) * d.
   * Q8_0, 34 bytes: fp16 d, then 32 int8; value = q * d.
+  * Q5_0, 22 bytes: fp16 d, qh[4], qs[16]; qs as in Q4_0, and bit j of the
+    little-endian word qh is weight j's fifth bit; value =
+    ((nibble | bit << 4) - 16) * d (tests/reference/ops.py:67-92, whose
+    split layout ql/qh/scales is these three fields pulled apart).
 
 The split conversion mirrors src/runtime/generate.py:91-119 (qs split out,
 fp16 d widened exactly to fp32).  The quantizers produce the synthetic
@@ -18,6 +22,7 @@ import numpy as np
 QK = 32
 Q4_0_BYTES = 18
 Q8_0_BYTES = 34
+Q5_0_BYTES = 22
 
 
 def _blocks(w: np.ndarray) -> np.ndarray:
@@ -108,3 +113,38 @@ def q4_0_nbytes(rows: int, K: int) -> int:
 
 def q8_0_nbytes(rows: int, K: int) -> int:
     return rows * (K // QK) * Q8_0_BYTES
+
+
+def q5_0_nbytes(rows: int, K: int) -> int:
+    return rows * (K // QK) * Q5_0_BYTES
+
+
+def pack_q5_0(ql: np.ndarray, qh: np.ndarray, d: np.ndarray) -> np.ndarray:
+    """Split Q5_0 (ql [rows, nb, 16], qh [rows, nb, 4], d [rows, nb] as
+    float16) -> GGUF blocks [rows, nb, 22]."""
+    ql = np.ascontiguousarray(ql, dtype=np.uint8)
+    rows, nb, _ = ql.shape
+    out = np.empty((rows, nb, Q5_0_BYTES), np.uint8)
+    out[..., 0:2] = np.ascontiguousarray(d, dtype=np.float16).reshape(rows, nb, 1).view(np.uint8)
+    out[..., 2:6] = qh
+    out[..., 6:] = ql
+    return out
+
+
+def split_q5_0(blocks: np.ndarray) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """GGUF Q5_0 blocks -> (ql [rows, nb, 16], qh [rows, nb, 4], scales
+    [rows, nb] float32), the layout asm_matmul_q5 reads."""
+    b = np.ascontiguousarray(blocks, dtype=np.uint8)
+    scales = np.ascontiguousarray(b[..., 0:2]).view(np.float16)[..., 0].astype(np.float32)
+    return np.ascontiguousarray(b[..., 6:]), np.ascontiguousarray(b[..., 2:6]), np.ascontiguousarray(scales)
+
+
+def dequantize_q5_0(blocks: np.ndarray) -> np.ndarray:
+    """Exact fp32 weights [rows, K]."""
+    ql, qh, scales = split_q5_0(blocks)
+    nib = np.concatenate([ql & 0x0F, ql >> 4], axis=-1).astype(np.int32)
+    word = qh.astype(np.uint32)
+    word = word[..., 0] | (word[..., 1] << 8) | (word[..., 2] << 16) | (word[..., 3] << 24)
+    bits = ((word[..., None] >> np.arange(32, dtype=np.uint32)) & 1).astype(np.int32)
+    w = (nib | (bits << 4)).astype(np.float32) - np.float32(16.0)
+    return (w * scales[..., None]).reshape(ql.shape[0], -1).astype(np.float32)

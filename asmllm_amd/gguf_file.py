@@ -11,8 +11,8 @@ only the vocabulary, and tensors are numpy views of a read-only memory map,
 so a multi-GB model is not copied before its one-time upload to the GPU.
 
 Tensor layouts (generate.py:169-180): dims[0] is the fastest (K) dimension,
-dims[1] the row count; Q4_0/Q8_0 tensors come back as [rows][K/32][18|34]
-uint8 blocks, F32/F16 as arrays of shape dims[::-1].
+dims[1] the row count; Q4_0/Q5_0/Q8_0 tensors come back as
+[rows][K/32][18|22|34] uint8 blocks, F32/F16 as arrays of shape dims[::-1].
 """
 
 from __future__ import annotations
@@ -24,7 +24,7 @@ from pathlib import Path
 
 import numpy as np
 
-from .gguf import Q4_0_BYTES, Q8_0_BYTES, QK
+from .gguf import Q4_0_BYTES, Q5_0_BYTES, Q8_0_BYTES, QK
 
 GGUF_MAGIC = 0x46554747  # "GGUF" little-endian
 DEFAULT_ALIGNMENT = 32
@@ -35,8 +35,9 @@ T_UINT8, T_INT8, T_UINT16, T_INT16, T_UINT32, T_INT32, T_FLOAT32, T_BOOL, T_STRI
 _SCALAR = {T_UINT8: "<B", T_INT8: "<b", T_UINT16: "<H", T_INT16: "<h", T_UINT32: "<I", T_INT32: "<i",
            T_FLOAT32: "<f", T_BOOL: "<?", T_UINT64: "<Q", T_INT64: "<q", T_FLOAT64: "<d"}
 
-# tensor types (GGUF / ggml numbering, generate.py:170-180)
-F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
+# tensor types (GGUF / ggml numbering, generate.py:170-180; Q5_0 is ggml's 6)
+F32, F16, Q4_0, Q5_0, Q8_0 = 0, 1, 2, 6, 8
+_BLOCK_BYTES = {Q4_0: Q4_0_BYTES, Q5_0: Q5_0_BYTES, Q8_0: Q8_0_BYTES}
 
 
 class GGUFError(ValueError):
@@ -57,10 +58,10 @@ class TensorInfo:
             return 4 * n
         if self.type == F16:
             return 2 * n
-        if self.type in (Q4_0, Q8_0):
+        if self.type in _BLOCK_BYTES:
             if self.dims[0] % QK:
                 raise GGUFError(f"{self.name}: K = {self.dims[0]} is not a multiple of 32")
-            return n // QK * (Q4_0_BYTES if self.type == Q4_0 else Q8_0_BYTES)
+            return n // QK * _BLOCK_BYTES[self.type]
         raise GGUFError(f"{self.name}: tensor type {self.type} is not supported")
 
 
@@ -152,8 +153,7 @@ class GGUFFile:
         if t.type == F16:
             return raw.view(np.float16).reshape(t.dims[::-1])
         rows = int(np.prod(t.dims[1:], dtype=np.int64)) if len(t.dims) > 1 else 1
-        width = Q4_0_BYTES if t.type == Q4_0 else Q8_0_BYTES
-        return raw.reshape(rows, t.dims[0] // QK, width)
+        return raw.reshape(rows, t.dims[0] // QK, _BLOCK_BYTES[t.type])
 
     def vocab(self) -> list[str]:
         """tokenizer.ggml.tokens (generate.py:71-76)."""

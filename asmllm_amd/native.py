@@ -20,6 +20,7 @@ _P = c_void_p
 
 # Values of the header's #defines.
 Q4_0 = 2
+Q5_0 = 6
 Q8_0 = 8
 PRE_NONE, PRE_RMSNORM, PRE_SWIGLU = 0, 1, 2
 Q4_KERNEL_AUTO, Q4_KERNEL_FP32, Q4_KERNEL_MFMA = 0, 1, 2
@@ -33,6 +34,9 @@ SIGNATURES: dict[str, tuple] = {
     "asm_matmul_q4_mt": (None, [_P, _P, _P, _P, c_int64, c_int64, c_int]),
     "asm_matmul_q8_mt": (None, [_P, _P, _P, _P, c_int64, c_int64, c_int]),
     "asm_threadpool_dispatch_q8": (None, [_P, _P, _P, _P, c_int64, c_int64]),
+    "asm_matmul_q5": (None, [_P, _P, _P, _P, _P, c_int64, c_int64]),
+    "asm_matmul_q5_mt": (None, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int]),
+    "asm_threadpool_dispatch_q5": (None, [_P, _P, _P, _P, _P, c_int64, c_int64]),
     "asm_threadpool_init": (None, [c_int]),
     "asm_threadpool_shutdown": (None, []),
     "asm_threadpool_get_num_threads": (c_int, []),
@@ -46,6 +50,9 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_matmul_q8_0": (c_int, [_P, _P, _P, c_int64, c_int64, _P]),
     "asmhip_matmul_q4_split": (c_int, [_P, _P, _P, _P, c_int64, c_int64, _P]),
     "asmhip_matmul_q8_split": (c_int, [_P, _P, _P, _P, c_int64, c_int64, _P]),
+    "asmhip_matmul_q5_split": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, _P]),
+    "asmhip_matmul_q5_0": (c_int, [_P, _P, _P, c_int64, c_int64, _P]),
+    "asmhip_dequantize_q5_0": (c_int, [_P, _P, c_int64, c_int64, _P]),
     "asmhip_dequantize_q4_0": (c_int, [_P, _P, c_int64, c_int64, _P]),
     "asmhip_dequantize_q8_0": (c_int, [_P, _P, c_int64, c_int64, _P]),
     "asmhip_matmul_fused": (c_int, [c_int, _P, _P, _P, c_int64, c_int64, c_int, _P, c_float, c_int, _P]),

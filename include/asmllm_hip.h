@@ -20,9 +20,12 @@
  *
  * Block layouts (GGUF):  Q4_0 = fp16 d + 16 bytes, byte j holding weight j
  * (low nibble) and weight j+16 (high nibble), value (nibble - 8) * d;
- * Q8_0 = fp16 d + 32 int8, value q * d.  Rows are [M][K/32] blocks.
+ * Q8_0 = fp16 d + 32 int8, value q * d; Q5_0 = fp16 d + qh[4] + qs[16], qs
+ * as in Q4_0 and bit j of the little-endian word qh weight j's fifth bit,
+ * value ((nibble | bit << 4) - 16) * d.  Rows are [M][K/32] blocks.
  * Split layout (the reference kernels' ABI): qs [M][K/32][16 or 32] bytes
- * plus fp32 scales [M][K/32].  K must be a multiple of 32.
+ * plus fp32 scales [M][K/32]; for Q5 ql [M][K/32][16] + qh [M][K/32][4] +
+ * fp32 scales.  K must be a multiple of 32.
  */
 #ifndef ASMLLM_HIP_H
 #define ASMLLM_HIP_H
@@ -45,6 +48,7 @@ extern "C" {
 
 /* Block types, numbered as GGUF tensor types (src/runtime/generate.py:175-178). */
 #define ASMHIP_Q4_0 2
+#define ASMHIP_Q5_0 6
 #define ASMHIP_Q8_0 8
 
 /* Work fused into a matvec's read of x (asmhip_matmul_fused). */
@@ -68,6 +72,10 @@ ASMHIP_API void asm_matmul_q4_avx512(const uint8_t* qweights, const float* scale
 /* src/kernels/x86_64/matmul_q8_avx2.asm:11-19, 51. */
 ASMHIP_API void asm_matmul_q8(const int8_t* qweights, const float* scales, const float* x, float* y,
                               int64_t M, int64_t K);
+/* src/kernels/x86_64/matmul_q5_avx2.asm:11-20, 52: y = W x, Q5_0 split layout
+ * (ql nibbles, qh fifth-bit planes, fp32 scales). */
+ASMHIP_API void asm_matmul_q5(const uint8_t* ql, const uint8_t* qh, const float* scales, const float* x,
+                              float* y, int64_t M, int64_t K);
 /* src/runtime/threadpool.h:49-57 / threadpool.c:390-486.  On the GPU one
  * launch covers all rows; num_threads only updates the recorded pool size
  * (threadpool.c:404-406), the result is bitwise the same for every value. */
@@ -79,6 +87,13 @@ ASMHIP_API void asm_matmul_q8_mt(const int8_t* qweights, const float* scales, co
 /* src/runtime/threadpool.h:80-87 / threadpool.c:588-665. */
 ASMHIP_API void asm_threadpool_dispatch_q8(const int8_t* qweights, const float* scales, const float* x,
                                            float* y, int64_t M, int64_t K);
+/* src/runtime/threadpool.h:69-78 / threadpool.c:769-787 (num_threads as for
+ * asm_matmul_q4_mt). */
+ASMHIP_API void asm_matmul_q5_mt(const uint8_t* ql, const uint8_t* qh, const float* scales, const float* x,
+                                 float* y, int64_t M, int64_t K, int num_threads);
+/* src/runtime/threadpool.h:89-97 / threadpool.c:667-748. */
+ASMHIP_API void asm_threadpool_dispatch_q5(const uint8_t* ql, const uint8_t* qh, const float* scales,
+                                           const float* x, float* y, int64_t M, int64_t K);
 /* src/runtime/threadpool.h:37 / threadpool.c:340-369: binds the calling
  * thread's current HIP device, creates the library stream and records the
  * pool size (clamped to [1, 64], threadpool.c:345-346). */
@@ -121,10 +136,18 @@ ASMHIP_API int asmhip_matmul_q4_split(const uint8_t* qweights, const float* scal
                                       float* y, int64_t M, int64_t K, void* stream);
 ASMHIP_API int asmhip_matmul_q8_split(const int8_t* qweights, const float* scales, const float* x,
                                       float* y, int64_t M, int64_t K, void* stream);
+/* Q5_0 matvecs on device pointers: the asm_matmul_q5 contract
+ * (matmul_q5_avx2.asm:93-210) on the split layout, and the same arithmetic
+ * over 22-byte GGUF Q5_0 blocks read in place (scale widened fp16 -> fp32). */
+ASMHIP_API int asmhip_matmul_q5_split(const uint8_t* ql, const uint8_t* qh, const float* scales, const float* x,
+                                      float* y, int64_t M, int64_t K, void* stream);
+ASMHIP_API int asmhip_matmul_q5_0(const void* blocks, const float* x, float* y, int64_t M, int64_t K,
+                                  void* stream);
 /* Exact fp32 dequantization of GGUF blocks into w[rows][K]
- * (tests/reference/ops.py:16-30, 44-53). */
+ * (tests/reference/ops.py:16-30, 44-53, 67-92). */
 ASMHIP_API int asmhip_dequantize_q4_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream);
 ASMHIP_API int asmhip_dequantize_q8_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream);
+ASMHIP_API int asmhip_dequantize_q5_0(const void* blocks, float* w, int64_t rows, int64_t K, void* stream);
 
 /* GGUF-block matvec with work fused around it, as forward_token sequences it
  * (generate.py:261-326): pre_op transforms x while it is read (RMSNorm with

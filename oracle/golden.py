@@ -37,10 +37,12 @@ def generate_reference_data(seed: int = 42) -> dict[str, np.ndarray]:
     d["q8_matmul_qweights"], d["q8_matmul_scales"], d["q8_matmul_x"] = q8, q8s, x
     d["q8_matmul_expected"] = ops_ref.q8_matmul(q8, q8s, x)
 
-    # :61-71 -- Q5 draws (Q5_0 is outside this build; drawn to keep the stream aligned)
-    rng.randint(0, 256, size=(4, 2, 16), dtype=np.uint8)
-    rng.randint(0, 256, size=(4, 2, 4), dtype=np.uint8)
-    rng.uniform(0.1, 1.5, size=(4, 2))
+    # :61-71 -- Q5, same x
+    q5l = rng.randint(0, 256, size=(4, 2, 16), dtype=np.uint8)
+    q5h = rng.randint(0, 256, size=(4, 2, 4), dtype=np.uint8)
+    q5s = rng.uniform(0.1, 1.5, size=(4, 2)).astype(np.float32)
+    d["q5_matmul_ql"], d["q5_matmul_qh"], d["q5_matmul_scales"], d["q5_matmul_x"] = q5l, q5h, q5s, x
+    d["q5_matmul_expected"] = ops_ref.q5_matmul(q5l, q5h, q5s, x)
 
     # :73-81 -- RMSNorm, dim 64, eps 1e-5
     xn = rng.randn(64).astype(np.float32)

@@ -20,6 +20,13 @@ _SIGS = {
     "oracle_matmul_q4_avx512_lanes": (None, [_P, _P, _P, _P, c_int64, c_int64]),
     "oracle_matmul_q8_avx2": (None, [_P, _P, _P, _P, c_int64, c_int64]),
     "oracle_matmul_q8_lanes": (None, [_P, _P, _P, _P, c_int64, c_int64]),
+    "oracle_matmul_q5_avx2": (None, [_P, _P, _P, _P, _P, c_int64, c_int64]),
+    "oracle_matmul_q5_lanes": (None, [_P, _P, _P, _P, _P, c_int64, c_int64]),
+    "oracle_matmul_q5_mt": (None, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int]),
+    "oracle_threadpool_dispatch_q5": (None, [_P, _P, _P, _P, _P, c_int64, c_int64]),
+    "oracle_matmul_q5_0_gguf": (None, [_P, _P, _P, c_int64, c_int64, c_int]),
+    "oracle_split_q5_0": (None, [_P, _P, _P, _P, c_int64, c_int64]),
+    "oracle_dequantize_q5_0": (None, [_P, _P, c_int64, c_int64]),
     "oracle_matmul_q4_0_gguf": (None, [_P, _P, _P, c_int64, c_int64, c_int]),
     "oracle_matmul_q8_0_gguf": (None, [_P, _P, _P, c_int64, c_int64, c_int]),
     "oracle_split_q4_0": (None, [_P, _P, _P, c_int64, c_int64]),
@@ -118,6 +125,23 @@ def matmul_q8_mt(qweights, scales, x, nt: int) -> np.ndarray:
     return y
 
 
+def matmul_q5(ql, qh, scales, x, kernel: str = "avx2") -> np.ndarray:
+    l, h, s, xv = _c(ql, np.uint8), _c(qh, np.uint8), _c(scales, np.float32), _c(x, np.float32)
+    M, K = l.shape[0], xv.shape[0]
+    y = np.zeros(M, np.float32)
+    fn = {"avx2": lib().oracle_matmul_q5_avx2, "lanes": lib().oracle_matmul_q5_lanes}[kernel]
+    fn(_ptr(l), _ptr(h), _ptr(s), _ptr(xv), _ptr(y), M, K)
+    return y
+
+
+def matmul_q5_mt(ql, qh, scales, x, nt: int) -> np.ndarray:
+    l, h, s, xv = _c(ql, np.uint8), _c(qh, np.uint8), _c(scales, np.float32), _c(x, np.float32)
+    M, K = l.shape[0], xv.shape[0]
+    y = np.zeros(M, np.float32)
+    lib().oracle_matmul_q5_mt(_ptr(l), _ptr(h), _ptr(s), _ptr(xv), _ptr(y), M, K, nt)
+    return y
+
+
 def tile_rows(M: int, nt: int) -> int:
     return int(lib().oracle_tile_rows(M, nt))
 
@@ -137,6 +161,14 @@ def matmul_q8_0_gguf(blocks, x, nt: int = 1) -> np.ndarray:
     M, K = b.shape[0], xv.shape[0]
     y = np.zeros(M, np.float32)
     lib().oracle_matmul_q8_0_gguf(_ptr(b), _ptr(xv), _ptr(y), M, K, nt)
+    return y
+
+
+def matmul_q5_0_gguf(blocks, x, nt: int = 1) -> np.ndarray:
+    b, xv = _c(blocks, np.uint8), _c(x, np.float32)
+    M, K = b.shape[0], xv.shape[0]
+    y = np.zeros(M, np.float32)
+    lib().oracle_matmul_q5_0_gguf(_ptr(b), _ptr(xv), _ptr(y), M, K, nt)
     return y
 
 
@@ -170,6 +202,25 @@ def dequantize_q8_0(blocks) -> np.ndarray:
     out = np.empty((rows, nb * 32), np.float32)
     lib().oracle_dequantize_q8_0(_ptr(b), _ptr(out), rows, nb * 32)
     return out
+
+
+def dequantize_q5_0(blocks) -> np.ndarray:
+    b = _c(blocks, np.uint8)
+    rows, nb = b.shape[0], b.shape[1]
+    out = np.empty((rows, nb * 32), np.float32)
+    lib().oracle_dequantize_q5_0(_ptr(b), _ptr(out), rows, nb * 32)
+    return out
+
+
+def split_q5_0(blocks):
+    """GGUF Q5_0 blocks [rows][nb][22] -> (ql [rows][nb][16], qh [rows][nb][4], fp32 scales)."""
+    b = _c(blocks, np.uint8)
+    rows, nb = b.shape[0], b.shape[1]
+    ql = np.empty((rows, nb, 16), np.uint8)
+    qh = np.empty((rows, nb, 4), np.uint8)
+    sc = np.empty((rows, nb), np.float32)
+    lib().oracle_split_q5_0(_ptr(b), _ptr(ql), _ptr(qh), _ptr(sc), rows, nb * 32)
+    return ql, qh, sc
 
 
 def split_q4_0(blocks):

@@ -41,6 +41,24 @@ def q8_matmul(qweights: np.ndarray, scales: np.ndarray, x: np.ndarray) -> np.nda
     return dequantize_q8_0(qweights, scales) @ x
 
 
+# ---- ops.py:67-99 ------------------------------------------------------------------
+
+def dequantize_q5_0(ql: np.ndarray, qh: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """(rows, nb, 16) nibbles + (rows, nb, 4) high-bit planes + (rows, nb)
+    fp32 scales -> (rows, nb*32).  Weight j's fifth bit is bit j % 8 of qh
+    byte j // 8; value ((nibble | bit << 4) - 16) * scale in float32."""
+    rows, nb, width = ql.shape
+    assert width == 16 and qh.shape == (rows, nb, 4)
+    nib = np.concatenate([ql & 0x0F, ql >> 4], axis=-1).astype(np.int32)
+    bits = np.unpackbits(qh, axis=-1, bitorder="little").astype(np.int32)
+    w = (nib | (bits << 4)).astype(np.float32) - np.float32(16.0)
+    return (w * scales[:, :, None]).reshape(rows, nb * 32)
+
+
+def q5_matmul(ql: np.ndarray, qh: np.ndarray, scales: np.ndarray, x: np.ndarray) -> np.ndarray:
+    return dequantize_q5_0(ql, qh, scales) @ x
+
+
 # ---- ops.py:103-170 ----------------------------------------------------------------
 
 def rmsnorm(x: np.ndarray, weight: np.ndarray, eps: float = 1e-5) -> np.ndarray:
@@ -103,6 +121,20 @@ def q8_matvec_f64(qweights: np.ndarray, scales: np.ndarray, x: np.ndarray) -> np
     xb = x.astype(np.float64).reshape(nb, 32)
     per_block = np.einsum("mbj,bj->mb", qweights.astype(np.float64), xb)
     return (per_block * scales.astype(np.float64)).sum(axis=1)
+
+
+def q5_matvec_f64(ql: np.ndarray, qh: np.ndarray, scales: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """y[m] = sum_b s[m,b] * sum_j ((n_j + 16 h_j) - 16) x[32b+j] in float64,
+    with n_j and h_j read element by element (ql byte j % 16, low nibble for
+    j < 16; bit j % 8 of qh byte j // 8), not through dequantize_q5_0."""
+    M, nb, _ = ql.shape
+    w = np.empty((M, nb, 32), np.float64)
+    for j in range(32):
+        n = (ql[:, :, j % 16] % 16) if j < 16 else (ql[:, :, j % 16] // 16)
+        h = (qh[:, :, j // 8] // (1 << (j % 8))) % 2
+        w[:, :, j] = n.astype(np.float64) + 16.0 * h.astype(np.float64) - 16.0
+    xb = x.astype(np.float64).reshape(nb, 32)
+    return (np.einsum("mbj,bj->mb", w, xb) * scales.astype(np.float64)).sum(axis=1)
 
 
 def row_l1(w_fp32: np.ndarray, x: np.ndarray) -> np.ndarray:

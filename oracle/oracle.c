@@ -323,6 +323,102 @@ FMA_FN void oracle_matmul_q8_lanes(const int8_t* q, const float* s, const float*
 }
 
 /* ======================================================================== */
+/* Q5_0 AVX2 kernel, matmul_q5_avx2.asm:93-210                              */
+/* ======================================================================== */
+
+/* One block (:104-193): the 16 ql bytes split into low nibbles (weights
+ * 0..15) and high nibbles (16..31, :117-124); slice k of eight weights takes
+ * qh byte k, broadcast and tested against 1,2,4,..,128 (:134-140), so that
+ * lane l adds 16.0 when bit l is set; the weight is cvt(nibble) + that - 16.0
+ * (:142-145), folded into a fresh accumulator by vfmadd231ps (:146). */
+AVX2_FN static inline __m256 q5_block_avx2(const uint8_t* ql, const uint8_t* qh, const float* xb) {
+    const __m128i m0f = _mm_set1_epi8(0x0F);
+    const __m256 sixteen = _mm256_set1_ps(16.0f);
+    const __m256i lane_bit = _mm256_setr_epi32(1, 2, 4, 8, 16, 32, 64, 128);
+    __m128i raw = _mm_loadu_si128((const __m128i*)ql);
+    __m128i lo = _mm_and_si128(raw, m0f);
+    __m128i hi = _mm_and_si128(_mm_srli_epi16(raw, 4), m0f);
+    const __m128i slice[4] = {lo, _mm_srli_si128(lo, 8), hi, _mm_srli_si128(hi, 8)};
+    __m256 t = _mm256_setzero_ps();
+    for (int k = 0; k < 4; ++k) {
+        __m256i sel = _mm256_and_si256(_mm256_set1_epi32(qh[k]), lane_bit);
+        __m256 add = _mm256_and_ps(_mm256_castsi256_ps(_mm256_cmpeq_epi32(sel, lane_bit)), sixteen);
+        __m256 w = _mm256_cvtepi32_ps(_mm256_cvtepu8_epi32(slice[k]));
+        w = _mm256_sub_ps(_mm256_add_ps(w, add), sixteen);
+        t = _mm256_fmadd_ps(w, _mm256_loadu_ps(xb + 8 * k), t);
+    }
+    return t;
+}
+
+/* Rows [r0, r1): per-block scale FMA (:196-197), then the horizontal sum of
+ * :202-210, the same order as hsum8. */
+AVX2_FN static void q5_avx2_rows(const uint8_t* ql, const uint8_t* qh, const float* s, const float* x, float* y,
+                                 int64_t r0, int64_t r1, int64_t K) {
+    int64_t nb = K / 32;
+    for (int64_t m = r0; m < r1; ++m) {
+        __m256 acc = _mm256_setzero_ps();
+        for (int64_t b = 0; b < nb; ++b) {
+            int64_t blk = m * nb + b;
+            __m256 t = q5_block_avx2(ql + blk * 16, qh + blk * 4, x + b * 32);
+            acc = _mm256_fmadd_ps(t, _mm256_set1_ps(s[blk]), acc);
+        }
+        y[m] = hsum8(acc);
+    }
+}
+
+/* GGUF Q5_0 blocks (22 B: fp16 d, qh[4], qs[16]) with the same arithmetic,
+ * the scale widened fp16 -> fp32 first. */
+AVX2_FN static void q5_0_gguf_avx2_rows(const uint8_t* blocks, const float* x, float* y, int64_t r0, int64_t r1,
+                                        int64_t K) {
+    int64_t nb = K / 32;
+    for (int64_t m = r0; m < r1; ++m) {
+        __m256 acc = _mm256_setzero_ps();
+        const uint8_t* row = blocks + m * nb * 22;
+        for (int64_t b = 0; b < nb; ++b) {
+            const uint8_t* blk = row + b * 22;
+            __m256 t = q5_block_avx2(blk + 6, blk + 2, x + b * 32);
+            acc = _mm256_fmadd_ps(t, _mm256_set1_ps(load_f16(blk)), acc);
+        }
+        y[m] = hsum8(acc);
+    }
+}
+
+void oracle_matmul_q5_avx2(const uint8_t* ql, const uint8_t* qh, const float* s, const float* x, float* y,
+                           int64_t M, int64_t K) {
+    q5_avx2_rows(ql, qh, s, x, y, 0, M, K);
+}
+
+/* The same arithmetic as eight scalar lanes: lane l of block b sees weights
+ * l, 8+l (low nibbles of bytes l, 8+l) and 16+l, 24+l (high nibbles), whose
+ * fifth bits are bit l of qh bytes 0, 1, 2, 3. */
+FMA_FN void oracle_matmul_q5_lanes(const uint8_t* ql, const uint8_t* qh, const float* s, const float* x, float* y,
+                                   int64_t M, int64_t K) {
+    int64_t nb = K / 32;
+    for (int64_t m = 0; m < M; ++m) {
+        float acc[8] = {0};
+        for (int64_t b = 0; b < nb; ++b) {
+            const uint8_t* q = ql + (m * nb + b) * 16;
+            const uint8_t* h = qh + (m * nb + b) * 4;
+            const float* xb = x + b * 32;
+            float sc = s[m * nb + b];
+            for (int l = 0; l < 8; ++l) {
+                float t = 0.0f;
+                for (int k = 0; k < 4; ++k) {
+                    int byte = (k & 1) * 8 + l;
+                    int nib = k < 2 ? (q[byte] & 15) : (q[byte] >> 4);
+                    float high = ((h[k] >> l) & 1) ? 16.0f : 0.0f;
+                    float w = ((float)nib + high) - 16.0f;
+                    t = fmaf(w, xb[8 * k + l], t);
+                }
+                acc[l] = fmaf(t, sc, acc[l]);
+            }
+        }
+        float a0 = acc[0] + acc[4], a1 = acc[1] + acc[5], a2 = acc[2] + acc[6], a3 = acc[3] + acc[7];
+        y[m] = (a0 + a2) + (a1 + a3);
+    }
+}
+
+/* ======================================================================== */
 /* a6/a7: GGUF block conversion and exact dequant                           */
 /* ======================================================================== */
 
@@ -362,6 +458,34 @@ void oracle_dequantize_q8_0(const uint8_t* blocks, float* w, int64_t rows, int64
         const uint8_t* blk = blocks + i * 34;
         float d = load_f16(blk);
         for (int j = 0; j < 32; ++j) w[i * 32 + j] = (float)(int8_t)blk[2 + j] * d;
+    }
+}
+
+/* GGUF Q5_0 blocks -> the split layout asm_matmul_q5 reads (ql, qh planes,
+ * fp32 scales): the byte planes are copied, the scale widened exactly. */
+void oracle_split_q5_0(const uint8_t* blocks, uint8_t* ql, uint8_t* qh, float* scales, int64_t rows, int64_t K) {
+    int64_t n = rows * (K / 32);
+    for (int64_t i = 0; i < n; ++i) {
+        const uint8_t* b = blocks + i * 22;
+        scales[i] = load_f16(b);
+        memcpy(qh + i * 4, b + 2, 4);
+        memcpy(ql + i * 16, b + 6, 16);
+    }
+}
+
+/* ops.py:67-92 applied to GGUF Q5_0 blocks. */
+void oracle_dequantize_q5_0(const uint8_t* blocks, float* w, int64_t rows, int64_t K) {
+    int64_t n = rows * (K / 32);
+    for (int64_t i = 0; i < n; ++i) {
+        const uint8_t* b = blocks + i * 22;
+        float d = load_f16(b);
+        uint32_t h = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+        for (int j = 0; j < 16; ++j) {
+            int lo = (b[6 + j] & 15) | (int)(((h >> j) & 1u) << 4);
+            int hi = (b[6 + j] >> 4) | (int)(((h >> (j + 16)) & 1u) << 4);
+            w[i * 32 + j] = ((float)lo - 16.0f) * d;
+            w[i * 32 + 16 + j] = ((float)hi - 16.0f) * d;
+        }
     }
 }
 
@@ -631,6 +755,41 @@ void oracle_matmul_q8_mt(const int8_t* q, const float* s, const float* x, float*
     oracle_threadpool_dispatch_q8(q, s, x, y, M, K);
 }
 
+/* threadpool.c:101-115: the Q5 task carries the qh plane beside ql. */
+typedef struct {
+    const uint8_t* ql;
+    const uint8_t* qh;
+} q5_planes;
+
+static void q5_avx2_rows_v(const void* q, const float* s, const float* x, float* y, int64_t r0, int64_t r1,
+                           int64_t K) {
+    const q5_planes* p = (const q5_planes*)q;
+    q5_avx2_rows(p->ql, p->qh, s, x, y, r0, r1, K);
+}
+
+/* threadpool.c:667-748: below 32 rows or one pool thread, one call;
+ * otherwise rows split into tiles of round_up(ceil(M/nt), 16) (:684-686). */
+void oracle_threadpool_dispatch_q5(const uint8_t* ql, const uint8_t* qh, const float* s, const float* x, float* y,
+                                   int64_t M, int64_t K) {
+    if (g_pool_size <= 1 || M < 32) {
+        q5_avx2_rows(ql, qh, s, x, y, 0, M, K);
+        return;
+    }
+    q5_planes p = {ql, qh};
+    dispatch_rows(q5_avx2_rows_v, &p, s, x, y, M, K);
+}
+
+/* threadpool.c:769-787. */
+void oracle_matmul_q5_mt(const uint8_t* ql, const uint8_t* qh, const float* s, const float* x, float* y, int64_t M,
+                         int64_t K, int nt) {
+    if (nt <= 1 || M < 32) {
+        q5_avx2_rows(ql, qh, s, x, y, 0, M, K);
+        return;
+    }
+    if (g_pool_size != nt) oracle_threadpool_init(nt);
+    oracle_threadpool_dispatch_q5(ql, qh, s, x, y, M, K);
+}
+
 void oracle_matmul_q4_0_gguf(const uint8_t* blocks, const float* x, float* y, int64_t M, int64_t K,
                              int nt) {
     if (nt <= 1 || M < 32) {
@@ -649,6 +808,21 @@ void oracle_matmul_q8_0_gguf(const uint8_t* blocks, const float* x, float* y, in
     }
     if (g_pool_size != nt) oracle_threadpool_init(nt);
     dispatch_rows(q8_0_gguf_rows_v, blocks, NULL, x, y, M, K);
+}
+
+static void q5_0_gguf_rows_v(const void* q, const float* s, const float* x, float* y, int64_t r0, int64_t r1,
+                             int64_t K) {
+    (void)s;
+    q5_0_gguf_avx2_rows((const uint8_t*)q, x, y, r0, r1, K);
+}
+
+void oracle_matmul_q5_0_gguf(const uint8_t* blocks, const float* x, float* y, int64_t M, int64_t K, int nt) {
+    if (nt <= 1 || M < 32) {
+        q5_0_gguf_avx2_rows(blocks, x, y, 0, M, K);
+        return;
+    }
+    if (g_pool_size != nt) oracle_threadpool_init(nt);
+    dispatch_rows(q5_0_gguf_rows_v, blocks, NULL, x, y, M, K);
 }
 
 /* ======================================================================== */

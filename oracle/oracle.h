@@ -48,6 +48,12 @@ ORACLE_API void oracle_matmul_q8_avx2(const int8_t* qweights, const float* scale
 ORACLE_API void oracle_matmul_q8_lanes(const int8_t* qweights, const float* scales,
                                        const float* x, float* y, int64_t M, int64_t K);
 
+/* matmul_q5_avx2.asm:93-210: ql nibbles + qh bit planes + fp32 scales. */
+ORACLE_API void oracle_matmul_q5_avx2(const uint8_t* ql, const uint8_t* qh, const float* scales,
+                                      const float* x, float* y, int64_t M, int64_t K);
+ORACLE_API void oracle_matmul_q5_lanes(const uint8_t* ql, const uint8_t* qh, const float* scales,
+                                       const float* x, float* y, int64_t M, int64_t K);
+
 /* ---- a6: GGUF blocks read in place (scale widened fp16 -> fp32) --------- */
 
 /* Q4_0 GGUF blocks (18 B: fp16 d + 16 B qs) with the a1 arithmetic; the
@@ -58,14 +64,21 @@ ORACLE_API void oracle_matmul_q4_0_gguf(const uint8_t* blocks, const float* x, f
 ORACLE_API void oracle_matmul_q8_0_gguf(const uint8_t* blocks, const float* x, float* y,
                                         int64_t M, int64_t K, int nt);
 
+/* GGUF Q5_0 blocks (22 B: fp16 d, qh[4], qs[16]) with the Q5 arithmetic. */
+ORACLE_API void oracle_matmul_q5_0_gguf(const uint8_t* blocks, const float* x, float* y,
+                                        int64_t M, int64_t K, int nt);
+
 /* generate.py:91-106 / :109-119: GGUF blocks -> split qs + fp32 scales. */
 ORACLE_API void oracle_split_q4_0(const uint8_t* blocks, uint8_t* qs, float* scales,
                                   int64_t rows, int64_t K);
 ORACLE_API void oracle_split_q8_0(const uint8_t* blocks, int8_t* qs, float* scales,
                                   int64_t rows, int64_t K);
-/* ops.py:16-30 / :44-53 applied to GGUF blocks: exact fp32 dequant. */
+ORACLE_API void oracle_split_q5_0(const uint8_t* blocks, uint8_t* ql, uint8_t* qh, float* scales,
+                                  int64_t rows, int64_t K);
+/* ops.py:16-30 / :44-53 / :67-92 applied to GGUF blocks: exact fp32 dequant. */
 ORACLE_API void oracle_dequantize_q4_0(const uint8_t* blocks, float* w, int64_t rows, int64_t K);
 ORACLE_API void oracle_dequantize_q8_0(const uint8_t* blocks, float* w, int64_t rows, int64_t K);
+ORACLE_API void oracle_dequantize_q5_0(const uint8_t* blocks, float* w, int64_t rows, int64_t K);
 
 /* ---- quantizers (data generation for the synthetic configs) ------------- */
 
@@ -93,6 +106,11 @@ ORACLE_API void oracle_matmul_q4_mt(const uint8_t* qweights, const float* scales
 ORACLE_API void oracle_matmul_q8_mt(const int8_t* qweights, const float* scales,
                                     const float* x, float* y, int64_t M, int64_t K,
                                     int num_threads);
+/* threadpool.c:769-787 and :667-748. */
+ORACLE_API void oracle_matmul_q5_mt(const uint8_t* ql, const uint8_t* qh, const float* scales,
+                                    const float* x, float* y, int64_t M, int64_t K, int num_threads);
+ORACLE_API void oracle_threadpool_dispatch_q5(const uint8_t* ql, const uint8_t* qh, const float* scales,
+                                              const float* x, float* y, int64_t M, int64_t K);
 ORACLE_API void oracle_threadpool_dispatch_q8(const int8_t* qweights, const float* scales,
                                               const float* x, float* y, int64_t M, int64_t K);
 

@@ -30,9 +30,12 @@ def _tensors(rng):
     w8 = gguf.quantize_q8_0((rng.standard_normal((5, 64)) * 0.02).astype(np.float32))
     norm = rng.standard_normal(96).astype(np.float32)
     h = rng.standard_normal((3, 7)).astype(np.float16)
+    w5 = gguf.pack_q5_0(rng.integers(0, 256, (6, 2, 16), dtype=np.uint8), rng.integers(0, 256, (6, 2, 4), dtype=np.uint8),
+                        (rng.standard_normal((6, 2)) * 0.01).astype(np.float16))
     return {
         "blk.0.attn_q.weight": (gf.Q4_0, (96, 24), w4),
         "blk.0.ffn_down.weight": (gf.Q8_0, (64, 5), w8),
+        "blk.0.attn_v.weight": (gf.Q5_0, (64, 6), w5),
         "output_norm.weight": (gf.F32, (96,), norm),
         "odd.f16": (gf.F16, (7, 3), h),
     }
@@ -64,6 +67,7 @@ def test_round_trip(tmp_path, alignment, version):
             np.testing.assert_array_equal(g.tensor(name), data.reshape(g.tensor(name).shape))
         assert g.tensor("blk.0.attn_q.weight").shape == (24, 3, 18)
         assert g.tensor("blk.0.ffn_down.weight").shape == (5, 2, 34)
+        assert g.tensor("blk.0.attn_v.weight").shape == (6, 2, 22)
         assert g.tensor("odd.f16").shape == (3, 7)
 
 

@@ -292,3 +292,132 @@ def test_attention_decode_f16_against_numpy(oracle):
         p = np.exp(s - s.max())
         ref = (p / p.sum()) @ v
         np.testing.assert_allclose(got[h], ref, rtol=0, atol=1e-6)
+
+
+# ---- Q5_0 (matmul_q5_avx2.asm, ops.py:67-99, threadpool.c:667-787) -------------------------
+
+def _rand_q5(rng, M, K):
+    ql = rng.integers(0, 256, size=(M, K // 32, 16), dtype=np.uint8)
+    qh = rng.integers(0, 256, size=(M, K // 32, 4), dtype=np.uint8)
+    s = rng.uniform(0.05, 0.25, size=(M, K // 32)).astype(np.float32)
+    return ql, qh, s
+
+
+@pytest.mark.parametrize("kernel", ["avx2", "lanes"])
+def test_q5_golden(oracle, golden, kernel):
+    y = oracle.matmul_q5(golden["q5_matmul_ql"], golden["q5_matmul_qh"], golden["q5_matmul_scales"],
+                         golden["q5_matmul_x"], kernel)
+    err = np.abs(y - golden["q5_matmul_expected"]).max()
+    assert err <= golden_mod.TOLERANCE_Q5
+    assert err <= 1e-4  # fp32 reassociation only
+
+
+def test_golden_q5_expected_against_float64(golden):
+    y64 = ops_ref.q5_matvec_f64(golden["q5_matmul_ql"], golden["q5_matmul_qh"], golden["q5_matmul_scales"],
+                                golden["q5_matmul_x"])
+    np.testing.assert_allclose(golden["q5_matmul_expected"], y64, rtol=0, atol=1e-4)
+
+
+def test_q5_dequant_known_answers():
+    # Block 0: ql byte j = j (low nibble j, high nibble 0); qh = 0x0000FFFF, so
+    # weights 0..15 get their fifth bit (j + 16 - 16 = j) and 16..31 do not (0 - 16).
+    ql = np.zeros((1, 2, 16), np.uint8)
+    qh = np.zeros((1, 2, 4), np.uint8)
+    ql[0, 0] = np.arange(16)
+    qh[0, 0] = [0xFF, 0xFF, 0x00, 0x00]
+    # Block 1: ql byte j = 0xF0 | 0x0F (both nibbles 15); qh = 0x80000001: weight 0
+    # (15 + 16 - 16 = 15) and weight 31 (15) high, the rest 15 - 16 = -1.
+    ql[0, 1] = 0xFF
+    qh[0, 1] = [0x01, 0x00, 0x00, 0x80]
+    s = np.array([[1.0, 0.5]], np.float32)
+    w = ops_ref.dequantize_q5_0(ql, qh, s)
+    expect0 = list(range(16)) + [-16] * 16
+    expect1 = [15] + [-1] * 30 + [15]
+    np.testing.assert_array_equal(w[0, :32], np.array(expect0, np.float32))
+    np.testing.assert_array_equal(w[0, 32:], np.array(expect1, np.float32) * np.float32(0.5))
+
+
+@pytest.mark.parametrize("M,K", [(1, 32), (7, 64), (33, 256), (64, 4096)])
+def test_q5_avx2_equals_lane_model(oracle, M, K):
+    rng = np.random.default_rng(M * 7 + K)
+    ql, qh, s = _rand_q5(rng, M, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    np.testing.assert_array_equal(oracle.matmul_q5(ql, qh, s, x, "avx2"), oracle.matmul_q5(ql, qh, s, x, "lanes"))
+
+
+@pytest.mark.parametrize("M,K", [(16, 4096), (8, 11008)])
+def test_q5_against_float64(oracle, M, K):
+    rng = np.random.default_rng(K + 5)
+    ql, qh, s = _rand_q5(rng, M, K)
+    x = rng.standard_normal(K).astype(np.float32)
+    assert_matvec_close(oracle.matmul_q5(ql, qh, s, x), ops_ref.q5_matvec_f64(ql, qh, s, x),
+                        ops_ref.dequantize_q5_0(ql, qh, s), x, rel=1e-6)
+
+
+@pytest.mark.parametrize("mistake", ["bit_order_reversed", "high_bits_from_low_half", "offset_8"])
+def test_q5_closed_form_catches_plausible_mistakes(oracle, mistake):
+    """Inputs that model a plausible misreading of the format must fail the bar."""
+    rng = np.random.default_rng(14)
+    ql, qh, s = _rand_q5(rng, 8, 256)
+    x = rng.standard_normal(256).astype(np.float32)
+    y64 = ops_ref.q5_matvec_f64(ql, qh, s, x)
+    l1 = ops_ref.row_l1(ops_ref.dequantize_q5_0(ql, qh, s), x)
+    if mistake == "bit_order_reversed":  # bit 7 - j % 8 instead of bit j % 8
+        reversed_bits = np.packbits(np.unpackbits(qh, axis=-1, bitorder="little"), axis=-1, bitorder="big")
+        bad = oracle.matmul_q5(ql, reversed_bits, s, x)
+    elif mistake == "high_bits_from_low_half":  # weights 16..31 reuse bits 0..15
+        qh2 = qh.copy()
+        qh2[..., 2:] = qh[..., :2]
+        bad = oracle.matmul_q5(ql, qh2, s, x)
+    else:  # (n | h << 4) - 8: the Q4 offset
+        bad = oracle.matmul_q5(ql, qh, s, x) + 8.0 * (s.astype(np.float64) * x.astype(np.float64).reshape(-1, 32)
+                                                      .sum(-1)).sum(-1)
+    assert np.any(np.abs(bad - y64) > 1e-4 * l1)
+
+
+def test_q5_special_cases(oracle):
+    rng = np.random.default_rng(15)
+    ql, qh, s = _rand_q5(rng, 6, 128)
+    x = rng.standard_normal(128).astype(np.float32)
+    # every weight 16: all nibbles 0 with the fifth bit set -> exactly zero
+    assert np.all(oracle.matmul_q5(np.zeros_like(ql), np.full_like(qh, 0xFF), s, x) == 0.0)
+    assert np.all(oracle.matmul_q5(ql, qh, np.zeros_like(s), x) == 0.0)
+    w = ops_ref.dequantize_q5_0(ql, qh, s)
+    for col in (0, 15, 16, 31, 32, 100):
+        e = np.zeros(128, np.float32)
+        e[col] = 1.0
+        np.testing.assert_array_equal(oracle.matmul_q5(ql, qh, s, e), w[:, col])
+
+
+def test_q5_mt_bitwise_and_small_m_fallback(oracle):
+    rng = np.random.default_rng(16)
+    ql, qh, s = _rand_q5(rng, 700, 256)
+    x = rng.standard_normal(256).astype(np.float32)
+    ref = oracle.matmul_q5(ql, qh, s, x)
+    for nt in (2, 4, 7):
+        np.testing.assert_array_equal(oracle.matmul_q5_mt(ql, qh, s, x, nt), ref)
+    oracle.threadpool_init(3)
+    np.testing.assert_array_equal(oracle.matmul_q5_mt(ql[:20], qh[:20], s[:20], x, 8), ref[:20])
+    assert oracle.threadpool_size() == 3
+
+
+def test_q5_gguf_equals_split_path(oracle):
+    from asmllm_amd import gguf
+
+    rng = np.random.default_rng(17)
+    ql, qh, _ = _rand_q5(rng, 40, 320)
+    d = (rng.standard_normal((40, 10)) * 0.01).astype(np.float16)
+    blocks = gguf.pack_q5_0(ql, qh, d)
+    l2, h2, sc = oracle.split_q5_0(blocks)
+    np.testing.assert_array_equal(l2, ql)
+    np.testing.assert_array_equal(h2, qh)
+    np.testing.assert_array_equal(sc, d.astype(np.float32))
+    for a, b in zip(gguf.split_q5_0(blocks), (ql, qh, d.astype(np.float32))):
+        np.testing.assert_array_equal(a, b)
+    x = rng.standard_normal(320).astype(np.float32)
+    ref = oracle.matmul_q5(ql, qh, sc, x)
+    np.testing.assert_array_equal(oracle.matmul_q5_0_gguf(blocks, x), ref)
+    np.testing.assert_array_equal(oracle.matmul_q5_0_gguf(blocks, x, nt=4), ref)
+    w = ops_ref.dequantize_q5_0(ql, qh, sc)
+    np.testing.assert_array_equal(oracle.dequantize_q5_0(blocks), w)
+    np.testing.assert_array_equal(gguf.dequantize_q5_0(blocks), w)
