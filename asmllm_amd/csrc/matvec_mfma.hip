@@ -339,9 +339,12 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
                     if (q < kUnitPieces) park_piece(wbuf, q, buf[d][k]);
                 }
                 __builtin_amdgcn_wave_barrier();
+                // the unit is parked: refill its registers before the compute,
+                // so the next unit's latency overlaps this unit's MFMAs
+                load_unit(buf[d], s + D);
+                __builtin_amdgcn_sched_barrier(0);
                 acc = chunk_dot_x<kUnitBlocks>(rowd, rowp, aq[j], xsr[j], acc);
                 __builtin_amdgcn_wave_barrier();
-                load_unit(buf[d], s + D);
                 if (j == PW - 1) {  // last unit of tile s / PW
                     const float acc2 = __shfl_down(acc, 16, 64);  // level 2 of row n
                     if (g == 0 && s < L) part[((s / PW) * NW + wave) * 16 + n] = fmaf(acc2, 9.313225746154785e-10f, acc);  // 2^-30
@@ -361,12 +364,13 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
                     if (q < kUnitPieces) park_piece(wbuf, q, buf[d][k]);
                 }
                 __builtin_amdgcn_wave_barrier();
+                load_unit(buf[d], s + D);
+                __builtin_amdgcn_sched_barrier(0);
                 const int i = s / per_w;
                 const int u = wave + NW * (s - i * per_w);
                 acc = chunk_dot<kUnitBlocks>(rowd, rowp, xdig + u * kUnitBlocks * kXStride + aoff,
                                              xscale + u * kUnitBlocks, acc);
                 __builtin_amdgcn_wave_barrier();
-                load_unit(buf[d], s + D);
                 if (s - i * per_w == per_w - 1) {  // last unit of tile slot i
                     const float acc2 = __shfl_down(acc, 16, 64);  // level 2 of row n
                     if (g == 0) part[(i * NW + wave) * 16 + n] = fmaf(acc2, 9.313225746154785e-10f, acc);  // 2^-30
