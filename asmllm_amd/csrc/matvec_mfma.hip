@@ -4,25 +4,29 @@
 // (the reference's asm_matmul_q4, src/kernels/x86_64/matmul_q4_avx2.asm:57-287,
 // over GGUF blocks read in place).
 //
-// One v_mfma_i32_16x16x32_i8 per (16 rows, one 32-weight block):
-//   B operand  lane (n, g): qs dword g of row n's block as signed bytes
-//              16 (q - 8): low nibbles (weights 4g..4g+3) and high nibbles
-//              (weights 16+4g..16+4g+3), two bit operations each, exact;
-//   A operand  lane (m, g): the same 8 positions of x in two fixed-point levels
-//              relative to 2^e > the block's largest |x|:
+// One v_mfma_i32_16x16x64_i8 per (16 rows, block pair 2p, 2p+1):
+//   B operand  lane (n, G), n the weight row, G the k-group: groups 0-1 take
+//              block 2p, groups 2-3 block 2p+1; group G covers qs bytes
+//              8h..8h+7 (h = G & 1) of row n's block as signed bytes
+//              16 (q - 8): low nibbles (weights 8h..8h+7) and high nibbles
+//              (weights 16+8h..16+8h+7), two bit operations per dword, exact;
+//   A operand  the same 16 positions of x in two fixed-point levels relative to
+//              2^e > the block's largest |x|:
 //                X1 = trunc(x 2^(30-e)),  X2 = trunc((x 2^(30-e) - X1) 2^30),
-//              each split into four signed base-256 digits: rows 0-3 hold X1,
-//              rows 4-7 hold X2 (rows 8-15 repeat rows 0-7);
-//   D          lane n of group g (g = 0, 1) holds row n's four exact int32
-//              digit dots of level g+1: value = 2^24 D0 + 2^16 D1 + 2^8 D2 + D3
-//              = sum_j X_j 16 (q_j - 8).  Level 1 accumulates in lanes 0-15 and
-//              level 2 in lanes 16-31 with the same scale 2^(e-34) d; the two
-//              are joined with a 2^-30 weight at the end.
+//              each split into four signed base-256 digits: rows 0-3 hold X1 and
+//              rows 4-7 X2 of block 2p (in groups 0-1, zero in groups 2-3),
+//              rows 8-15 the same for block 2p+1 (in groups 2-3);
+//   D          lanes 0-15 / 16-31 hold row n's four exact int32 digit dots of
+//              level 1 / 2 of block 2p, lanes 32-47 / 48-63 those of block 2p+1:
+//              value = 2^24 D0 + 2^16 D1 + 2^8 D2 + D3 = sum_j X_j 16 (q_j - 8),
+//              scaled by 2^(e-34) d of the lane's block; every lane's epilogue is
+//              useful, and the four lane groups of a row are joined at the end
+//              of a tile (level 2 with a 2^-30 weight).
 // Per weight, x is exact to 2^-60 of its block's largest |x| (truncation); the
 // remaining error is fp32 rounding of per-block values, so a row stays within
 // ~1e-7 of sum |w| |x| of an fp32 evaluation unless x spans more than 2^56
 // inside one 32-block.  Every instruction above runs once per MFMA whichever
-// level a lane holds, so the second level costs only x preparation and LDS.
+// level or block a lane holds, so the second level costs only x preparation.
 //
 // Work mapping (persistent stream): one workgroup of NW waves per compute
 // unit.  Workgroup b owns the 16-row tiles b, b + G, b + 2G, ... (G = grid
@@ -60,7 +64,8 @@ constexpr int kRowPitch = 152;                     // LDS bytes per staged row: 
                                                    // 32 distinct banks (a 144-byte pitch pairs rows
                                                    // n and n + 8 on one bank)
 constexpr int kSlotBytes = 16 * kRowPitch;         // 2432: LDS slot per wave
-constexpr int kXStride = 264;                      // LDS bytes of x digits per block: [g][level*4+digit][8] + 8 pad
+constexpr int kXStride = 272;                      // LDS bytes of x digits per block: [half][level*4+digit][16] + 16 pad
+                                                   // (16-byte rows for the 16-byte A operands)
                                                    // (the pad staggers blocks across banks: conflict-free 8-byte writes)
 constexpr int kMaxBlocks = 512;                    // K <= 16384
 constexpr int kMaxTilesPerGroup = 8;
@@ -110,49 +115,92 @@ __device__ __forceinline__ float block_value(v4i d) {
     return fmaf((float)hi, 65536.0f, (float)lo);
 }
 
-// Row n's dot with x over NB staged blocks (NB even), for the lane (n, g),
-// with the lane's A operands aq[] and block scales xs[] given: every weight
-// operand is read from LDS first, then the MFMAs issue back to back, then the
-// per-block epilogues; no branch separates them.
+// One v_mfma_i32_16x16x64_i8 per block pair (2p, 2p + 1) of 16 staged rows.
+// Lane (n, G): n = lane & 15 is the weight row (B column), G = lane >> 4 the
+// k-group.  Groups 0-1 carry block 2p, groups 2-3 block 2p + 1; group G covers
+// positions 8h..8h+7 and 16+8h..16+8h+7 of its block (h = G & 1).  A rows 0-7
+// hold block 2p's x digits (levels 1, 2) in groups 0-1 and zeros in groups
+// 2-3; rows 8-15 the reverse for block 2p + 1.  So D lanes 0-15 / 16-31 hold
+// the level 1 / level 2 digit dots of block 2p and lanes 32-47 / 48-63 those
+// of block 2p + 1: every lane's epilogue is useful work.
+struct PairLane {
+    int bp;       // 0: this lane's block is the even one of the pair, 1: the odd one
+    int qoff;     // byte offset (dword aligned) of the lane's qs bytes in the pair's 36 bytes
+    uint32_t sh;  // alignbyte shift: 2 for the even block (qs two bytes off the dword grid), 0 for the odd
+    int doff;     // byte offset of the dword holding the block's fp16 scale
+    uint32_t dsh; // shift of that scale inside the dword
+};
+
+__device__ __forceinline__ PairLane pair_lane(int lane) {
+    const int G = lane >> 4, bp = G >> 1, h = G & 1;
+    PairLane pl;
+    pl.bp = bp;
+    pl.qoff = bp ? 20 + 8 * h : 8 * h;  // (2 + 8h) & ~3 for the even block, 20 + 8h for the odd
+    pl.sh = bp ? 0u : 2u;
+    pl.doff = 16 * bp;
+    pl.dsh = 16u * (uint32_t)bp;
+    return pl;
+}
+
+// Row n's dot with x over NB staged blocks (NB even), given the lane's A
+// operands aq[p] and block x-scales xs[p] (of the lane's block of pair p):
+// every weight operand is read from LDS first, then the MFMAs issue back to
+// back, then the per-pair epilogues.
 template <int NB>
-__device__ __forceinline__ float chunk_dot_x(const uint8_t* rowd, const uint8_t* rowp, const long* aq,
+__device__ __forceinline__ float chunk_dot_x(const uint8_t* rowd, const PairLane& pl, const v4i* aq,
                                              const float* xs, float acc) {
     constexpr int NP = NB / 2;
-    long bq[NB];
-    uint32_t sc[NP][2];
+    v4i bq[NP];
+    uint32_t sc[NP];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-        // blocks 2p (bytes 36p..) and 2p+1 (bytes 36p+18..) of row n
-        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(rowp + 36 * p);
-        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(rowp + 36 * p + 4);
-        const uint32_t w5 = *reinterpret_cast<const uint32_t*>(rowp + 36 * p + 20);
-        bq[2 * p] = pack_q4(__builtin_amdgcn_alignbyte(w1, w0, 2));
-        bq[2 * p + 1] = pack_q4(w5);
-        // fp16 scales of the two blocks (low half, high half); the same for every lane group
-        sc[p][0] = *reinterpret_cast<const uint32_t*>(rowd + 36 * p);
-        sc[p][1] = *reinterpret_cast<const uint32_t*>(rowd + 36 * p + 16);
+        const uint8_t* q = rowd + 36 * p + pl.qoff;
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(q);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(q + 4);
+        const uint32_t w2 = *reinterpret_cast<const uint32_t*>(q + 8);
+        const uint32_t qa = __builtin_amdgcn_alignbyte(w1, w0, pl.sh);
+        const uint32_t qb = __builtin_amdgcn_alignbyte(w2, w1, pl.sh);
+        const long la = pack_q4(qa), lb = pack_q4(qb);  // (lo | hi << 32) of each dword
+        bq[p] = (v4i){(int)(uint32_t)la, (int)(uint32_t)lb, (int)(uint32_t)(la >> 32), (int)(uint32_t)(lb >> 32)};
+        sc[p] = *reinterpret_cast<const uint32_t*>(rowd + 36 * p + pl.doff) >> pl.dsh;
     }
     const v4i z = {0, 0, 0, 0};
-    v4i d[NB];
+    v4i d[NP];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) d[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aq[j], bq[j], z, 0, 0, 0);
-    float acc1 = 0.f;
+    for (int p = 0; p < NP; ++p) d[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aq[p], bq[p], z, 0, 0, 0);
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        acc = fmaf(block_value(d[2 * p]) * xs[2 * p], half_lo(sc[p][0]), acc);
-        acc1 = fmaf(block_value(d[2 * p + 1]) * xs[2 * p + 1], half_hi(sc[p][1]), acc1);
-    }
-    return acc + acc1;
+    for (int p = 0; p < NP; ++p) acc = fmaf(block_value(d[p]) * xs[p], half_lo(sc[p]), acc);
+    return acc;
+}
+
+// Byte offset of this lane's A operand inside a block pair's digits; -1 where
+// the operand is zero (rows 0-7 in groups 2-3, rows 8-15 in groups 0-1).
+__device__ __forceinline__ int a_offset(int lane) {
+    const int n = lane & 15, G = lane >> 4;
+    if ((n < 8) != (G < 2)) return -1;
+    return (G >> 1) * kXStride + (G & 1) * 128 + (n & 7) * 16;
 }
 
 // The same with the A operands read from the x digits in LDS.
 template <int NB>
-__device__ __forceinline__ float chunk_dot(const uint8_t* rowd, const uint8_t* rowp, const uint8_t* xa,
-                                           const float* xs, float acc) {
-    long aq[NB];
+__device__ __forceinline__ float chunk_dot(const uint8_t* rowd, const PairLane& pl, const uint8_t* xu, int aoff,
+                                           const float* xsu, float acc) {
+    constexpr int NP = NB / 2;
+    v4i aq[NP];
+    float xs[NP];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) aq[j] = *reinterpret_cast<const long*>(xa + j * kXStride);
-    return chunk_dot_x<NB>(rowd, rowp, aq, xs, acc);
+    for (int p = 0; p < NP; ++p) {
+        aq[p] = aoff >= 0 ? *reinterpret_cast<const v4i*>(xu + 2 * p * kXStride + aoff) : (v4i){0, 0, 0, 0};
+        xs[p] = xsu[2 * p + pl.bp];
+    }
+    return chunk_dot_x<NB>(rowd, pl, aq, xs, acc);
+}
+
+// Row n's total from the lanes of a finished tile: level 1 + level 2 * 2^-30
+// over the even and odd blocks (valid in lanes 0-15).
+__device__ __forceinline__ float tile_total(float acc) {
+    acc += __shfl_down(acc, 32, 64);                                        // + odd blocks
+    return fmaf(__shfl_down(acc, 16, 64), 9.313225746154785e-10f, acc);     // + 2^-30 level 2
 }
 
 // PW > 0: every wave streams exactly PW units of each tile (K = 256 NW PW), so
@@ -295,13 +343,17 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
         transpose_digits(Y2, d2l);
         transpose_digits(Y2 + 4, d2h);
         if (it < ni) {
-            // row r of this lane's A operand: 8 bytes at g * 64 + 8 r; rows 0-3 X1, 4-7 X2, top digit first
+            // digit row r (0-3 X1, 4-7 X2, top digit first) of half hh = g / 2 of block b:
+            // 16 bytes at hh * 128 + 16 r; positions 4g..4g+3 go to bytes 4 (g & 1) ..,
+            // positions 16+4g..16+4g+3 to bytes 8 + 4 (g & 1) ..
             const int b = it >> 2, g = it & 3;
-            uint64_t* base = reinterpret_cast<uint64_t*>(xdig + b * kXStride + g * 64);
+            uint32_t* base = reinterpret_cast<uint32_t*>(xdig + b * kXStride + (g >> 1) * 128) + (g & 1);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                base[k] = ((uint64_t)d1h[3 - k] << 32) | d1l[3 - k];
-                base[4 + k] = ((uint64_t)d2h[3 - k] << 32) | d2l[3 - k];
+                base[4 * k] = d1l[3 - k];
+                base[4 * k + 2] = d1h[3 - k];
+                base[4 * (4 + k)] = d2l[3 - k];
+                base[4 * (4 + k) + 2] = d2h[3 - k];
             }
             if (g == 0) xscale[b] = ldexpf(1.0f, e - 34);  // 2^(e-30) for X1, 1/16 for the weight bytes
         }
@@ -309,22 +361,23 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
     __syncthreads();
 
     // 4) the stream: stage unit s, multiply, refill its buffer with unit s + D.
-    const int n = lane & 15, g = lane >> 4;
-    const int aoff = g * 64 + (n & 7) * 8;
+    constexpr int kPairs = kUnitBlocks / 2;
+    const int n = lane & 15;
+    const int aoff = a_offset(lane);
+    const PairLane pl = pair_lane(lane);
     const uint8_t* rowd = wbuf + n * kRowPitch;      // row n's staged blocks (scales at 18 j)
-    const uint8_t* rowp = rowd + 4 * g;              // this lane's qs dword
     float acc = 0.f;
     if constexpr (PW > 0) {
         static_assert(D % PW == 0 || PW % D == 0, "the load ring and the tile's units align");
-        long aq[PW][kUnitBlocks];
-        float xsr[PW][kUnitBlocks];
+        v4i aq[PW][kPairs];
+        float xsr[PW][kPairs];
 #pragma unroll
         for (int j = 0; j < PW; ++j)
 #pragma unroll
-            for (int b = 0; b < kUnitBlocks; ++b) {
-                const int blk = (wave + NW * j) * kUnitBlocks + b;
-                aq[j][b] = *reinterpret_cast<const long*>(xdig + blk * kXStride + aoff);
-                xsr[j][b] = xscale[blk];
+            for (int p = 0; p < kPairs; ++p) {
+                const int blk = (wave + NW * j) * kUnitBlocks + 2 * p;
+                aq[j][p] = aoff >= 0 ? *reinterpret_cast<const v4i*>(xdig + blk * kXStride + aoff) : (v4i){0, 0, 0, 0};
+                xsr[j][p] = xscale[blk + pl.bp];
             }
         // whole rounds of max(D, PW) units: units past the stream's end were
         // loaded as zeros and only their partial-sum writes are skipped
@@ -343,11 +396,11 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
                 // so the next unit's latency overlaps this unit's MFMAs
                 load_unit(buf[d], s + D);
                 __builtin_amdgcn_sched_barrier(0);
-                acc = chunk_dot_x<kUnitBlocks>(rowd, rowp, aq[j], xsr[j], acc);
+                acc = chunk_dot_x<kUnitBlocks>(rowd, pl, aq[j], xsr[j], acc);
                 __builtin_amdgcn_wave_barrier();
                 if (j == PW - 1) {  // last unit of tile s / PW
-                    const float acc2 = __shfl_down(acc, 16, 64);  // level 2 of row n
-                    if (g == 0 && s < L) part[((s / PW) * NW + wave) * 16 + n] = fmaf(acc2, 9.313225746154785e-10f, acc);  // 2^-30
+                    const float t = tile_total(acc);
+                    if (lane < 16 && s < L) part[((s / PW) * NW + wave) * 16 + n] = t;
                     acc = 0.f;
                 }
             }
@@ -368,12 +421,12 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
                 __builtin_amdgcn_sched_barrier(0);
                 const int i = s / per_w;
                 const int u = wave + NW * (s - i * per_w);
-                acc = chunk_dot<kUnitBlocks>(rowd, rowp, xdig + u * kUnitBlocks * kXStride + aoff,
+                acc = chunk_dot<kUnitBlocks>(rowd, pl, xdig + u * kUnitBlocks * kXStride, aoff,
                                              xscale + u * kUnitBlocks, acc);
                 __builtin_amdgcn_wave_barrier();
                 if (s - i * per_w == per_w - 1) {  // last unit of tile slot i
-                    const float acc2 = __shfl_down(acc, 16, 64);  // level 2 of row n
-                    if (g == 0) part[(i * NW + wave) * 16 + n] = fmaf(acc2, 9.313225746154785e-10f, acc);  // 2^-30
+                    const float t = tile_total(acc);
+                    if (lane < 16) part[(i * NW + wave) * 16 + n] = t;
                     acc = 0.f;
                 }
             }
