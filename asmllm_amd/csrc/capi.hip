@@ -598,7 +598,14 @@ extern "C" int asmhip_embed_q4_0(const void* table, const int* token_dev, float*
                                  void* stream) {
     if (!table || !token_dev || !x) return fail(kInvalidArgument, "null pointer argument");
     if (n_vocab <= 0 || dim <= 0) return fail(kInvalidArgument, "bad embedding shape");
-    return embed_q4_0_launch(table, token_dev, x, n_vocab, dim, (hipStream_t)stream);
+    return embed_launch(QuantType::Q4_0, table, token_dev, x, n_vocab, dim, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_embed_q8_0(const void* table, const int* token_dev, float* x, int n_vocab, int dim,
+                                 void* stream) {
+    if (!table || !token_dev || !x) return fail(kInvalidArgument, "null pointer argument");
+    if (n_vocab <= 0 || dim <= 0) return fail(kInvalidArgument, "bad embedding shape");
+    return embed_launch(QuantType::Q8_0, table, token_dev, x, n_vocab, dim, (hipStream_t)stream);
 }
 
 extern "C" int asmhip_argmax(const float* logits, int n, int* token_dev, int* pos_dev, void* stream) {

@@ -198,12 +198,45 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(const float* __restri
 // rounded to fp16 and written to the caches at `pos` (by the workgroup of the
 // first query head of the kv group), and the workgroup whose split holds `pos`
 // uses those fp16 values instead of reading the row it writes.
+// E fp16 values of one cache row slice (E = 8: one 16-byte access; E = 6: three dwords).
+template <int E>
+struct HalfRow {
+    uint32_t w[E / 2];
+    __device__ static HalfRow load(const __half* p) {
+        HalfRow r;
+        if constexpr (E == 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(p);
+            r.w[0] = v.x, r.w[1] = v.y, r.w[2] = v.z, r.w[3] = v.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < E / 2; ++i) r.w[i] = reinterpret_cast<const uint32_t*>(p)[i];
+        }
+        return r;
+    }
+    __device__ static HalfRow zero() {
+        HalfRow r;
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) r.w[i] = 0u;
+        return r;
+    }
+    __device__ void store(__half* p) const {
+        if constexpr (E == 8) {
+            *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < E / 2; ++i) reinterpret_cast<uint32_t*>(p)[i] = w[i];
+        }
+    }
+};
+
 template <int HD, bool ROPE>
 __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __restrict__ qkv, __half* kc, __half* vc,
                                                              float* __restrict__ part, int n_heads, int n_kv,
                                                              const int* __restrict__ pos_ptr, int max_ctx,
                                                              float theta) {
-    constexpr int kLanes = HD / 8;                        // lanes per position
+    constexpr int E = HD % 64 == 0 ? 8 : 6;               // fp16 elements per lane
+    constexpr int kLanes = HD / E;                        // lanes per position
+    static_assert(HD == E * kLanes && kWave % kLanes == 0, "head_dim 48, 64 or 128");
     constexpr int kGroups = kWave / kLanes;               // positions per wave and row
     constexpr int kRowPos = kGroups * (kBlock / kWave);   // positions per workgroup and row
     constexpr int kRows = kAttnSplitLen / kRowPos;
@@ -218,22 +251,22 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     const int p0 = split * kAttnSplitLen, p1 = min(p0 + kAttnSplitLen, n_pos);
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
     const int g = lane / kLanes, c = lane % kLanes;
-    const size_t head_off = (size_t)kvh * max_ctx * HD + 8 * c;
+    const size_t head_off = (size_t)kvh * max_ctx * HD + E * c;
 
     // all k and v rows of this lane, issued up front
-    uint4 kr[kRows], vr[kRows];
+    HalfRow<E> kr[kRows], vr[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         const int p = p0 + r * kRowPos + w * kGroups + g;
         const bool live = p < p1 && !(ROPE && p == pos);
-        kr[r] = live ? *reinterpret_cast<const uint4*>(kc + head_off + (size_t)p * HD) : make_uint4(0, 0, 0, 0);
-        vr[r] = live ? *reinterpret_cast<const uint4*>(vc + head_off + (size_t)p * HD) : make_uint4(0, 0, 0, 0);
+        kr[r] = live ? HalfRow<E>::load(kc + head_off + (size_t)p * HD) : HalfRow<E>::zero();
+        vr[r] = live ? HalfRow<E>::load(vc + head_off + (size_t)p * HD) : HalfRow<E>::zero();
     }
-    float qv[8];
-    {
-        const float4 a = *reinterpret_cast<const float4*>(qkv + (size_t)h * HD + 8 * c);
-        const float4 b = *reinterpret_cast<const float4*>(qkv + (size_t)h * HD + 8 * c + 4);
-        qv[0] = a.x, qv[1] = a.y, qv[2] = a.z, qv[3] = a.w, qv[4] = b.x, qv[5] = b.y, qv[6] = b.z, qv[7] = b.w;
+    float qv[E];
+#pragma unroll
+    for (int t = 0; t < E; t += 2) {
+        const float2 a = *reinterpret_cast<const float2*>(qkv + (size_t)h * HD + E * c + t);
+        qv[t] = a.x, qv[t + 1] = a.y;
     }
     if constexpr (ROPE) {
         if (threadIdx.x < HD / 2 && n_pos > 0)
@@ -241,50 +274,48 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
         __syncthreads();
         if (n_pos > 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) rotate(&qv[2 * i], cs[2 * (4 * c + i)], cs[2 * (4 * c + i) + 1]);
+            for (int i = 0; i < E / 2; ++i) rotate(&qv[2 * i], cs[2 * (E / 2 * c + i)], cs[2 * (E / 2 * c + i) + 1]);
         }
         if (p0 <= pos && pos < p1) {
             // the new row: rotated k and v of kv head kvh, rounded to fp16
-            const float* kn = qkv + (size_t)(n_heads + kvh) * HD + 8 * c;
-            const float* vn = qkv + (size_t)(n_heads + n_kv + kvh) * HD + 8 * c;
-            uint32_t kw[4], vw[4];
+            const float* kn = qkv + (size_t)(n_heads + kvh) * HD + E * c;
+            const float* vn = qkv + (size_t)(n_heads + n_kv + kvh) * HD + E * c;
+            HalfRow<E> kq, vq;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < E / 2; ++i) {
                 float kk[2] = {kn[2 * i], kn[2 * i + 1]};
-                rotate(kk, cs[2 * (4 * c + i)], cs[2 * (4 * c + i) + 1]);
-                kw[i] = (uint32_t)__half_as_ushort(__float2half_rn(kk[0])) |
-                        ((uint32_t)__half_as_ushort(__float2half_rn(kk[1])) << 16);
-                vw[i] = (uint32_t)__half_as_ushort(__float2half_rn(vn[2 * i])) |
-                        ((uint32_t)__half_as_ushort(__float2half_rn(vn[2 * i + 1])) << 16);
+                rotate(kk, cs[2 * (E / 2 * c + i)], cs[2 * (E / 2 * c + i) + 1]);
+                kq.w[i] = (uint32_t)__half_as_ushort(__float2half_rn(kk[0])) |
+                          ((uint32_t)__half_as_ushort(__float2half_rn(kk[1])) << 16);
+                vq.w[i] = (uint32_t)__half_as_ushort(__float2half_rn(vn[2 * i])) |
+                          ((uint32_t)__half_as_ushort(__float2half_rn(vn[2 * i + 1])) << 16);
             }
-            const uint4 kq = make_uint4(kw[0], kw[1], kw[2], kw[3]), vq = make_uint4(vw[0], vw[1], vw[2], vw[3]);
             const int rr = (pos - p0) / kRowPos, rem = (pos - p0) % kRowPos;
             if (w == rem / kGroups && g == rem % kGroups) {
 #pragma unroll
                 for (int r = 0; r < kRows; ++r)
                     if (r == rr) kr[r] = kq, vr[r] = vq;
                 if (h % group == 0) {
-                    *reinterpret_cast<uint4*>(kc + head_off + (size_t)pos * HD) = kq;
-                    *reinterpret_cast<uint4*>(vc + head_off + (size_t)pos * HD) = vq;
+                    kq.store(kc + head_off + (size_t)pos * HD);
+                    vq.store(vc + head_off + (size_t)pos * HD);
                 }
             }
         }
     }
     const float scale = 1.0f / sqrtf((float)HD);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) qv[t] *= scale;
+    for (int t = 0; t < E; ++t) qv[t] *= scale;
 
     // scores of this lane group's positions, then its softmax state
     float sc[kRows];
     float m = -INFINITY;
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
-        const uint32_t kw[4] = {kr[r].x, kr[r].y, kr[r].z, kr[r].w};
         float d = 0.f;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            d = fmaf(qv[2 * t], half_lo(kw[t]), d);
-            d = fmaf(qv[2 * t + 1], half_hi(kw[t]), d);
+        for (int t = 0; t < E / 2; ++t) {
+            d = fmaf(qv[2 * t], half_lo(kr[r].w[t]), d);
+            d = fmaf(qv[2 * t + 1], half_hi(kr[r].w[t]), d);
         }
 #pragma unroll
         for (int o = kLanes / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, kWave);
@@ -292,17 +323,18 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
         sc[r] = p < p1 ? d : -INFINITY;
         m = fmaxf(m, sc[r]);
     }
-    float l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float l = 0.f, acc[E];
+#pragma unroll
+    for (int t = 0; t < E; ++t) acc[t] = 0.f;
     if (m != -INFINITY) {
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
             const float e = expf(sc[r] - m);  // 0 for positions past the split
             l += e;
-            const uint32_t vw[4] = {vr[r].x, vr[r].y, vr[r].z, vr[r].w};
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                acc[2 * t] = fmaf(e, half_lo(vw[t]), acc[2 * t]);
-                acc[2 * t + 1] = fmaf(e, half_hi(vw[t]), acc[2 * t + 1]);
+            for (int t = 0; t < E / 2; ++t) {
+                acc[2 * t] = fmaf(e, half_lo(vr[r].w[t]), acc[2 * t]);
+                acc[2 * t + 1] = fmaf(e, half_hi(vr[r].w[t]), acc[2 * t + 1]);
             }
         }
     }
@@ -314,12 +346,12 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
         const float f1 = M == -INFINITY ? 0.f : expf(m - M), f2 = M == -INFINITY ? 0.f : expf(m2 - M);
         l = l * f1 + l2 * f2;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) acc[t] = acc[t] * f1 + __shfl_xor(acc[t], o, kWave) * f2;
+        for (int t = 0; t < E; ++t) acc[t] = acc[t] * f1 + __shfl_xor(acc[t], o, kWave) * f2;
         m = M;
     }
     if (g == 0) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) wst[w][2 + 8 * c + t] = acc[t];
+        for (int t = 0; t < E; ++t) wst[w][2 + E * c + t] = acc[t];
         if (c == 0) wst[w][0] = m, wst[w][1] = l;
     }
     __syncthreads();
@@ -351,9 +383,9 @@ __global__ __launch_bounds__(HD) void attn_decode_merge(const float* __restrict_
     __shared__ float sm[64], sl[64];
     const int h = blockIdx.x;
     const float* ph = part + (size_t)h * S * (HD + 2);
-    if (threadIdx.x < S) {  // S <= 64, checked at launch
-        sm[threadIdx.x] = ph[(size_t)threadIdx.x * (HD + 2)];
-        sl[threadIdx.x] = ph[(size_t)threadIdx.x * (HD + 2) + 1];
+    for (int i = threadIdx.x; i < S; i += HD) {  // S <= 64, checked at launch
+        sm[i] = ph[(size_t)i * (HD + 2)];
+        sl[i] = ph[(size_t)i * (HD + 2) + 1];
     }
     __syncthreads();
     float M = -INFINITY;
@@ -371,17 +403,22 @@ __global__ __launch_bounds__(HD) void attn_decode_merge(const float* __restrict_
 }
 
 // ---- embedding row of a Q4_0 table -----------------------------------------------------
-__global__ __launch_bounds__(kBlock) void embed_q4_0_kernel(const uint8_t* __restrict__ table,
-                                                            const int* __restrict__ token, float* __restrict__ x,
-                                                            int n_vocab, int dim) {
+template <bool kQ8>
+__global__ __launch_bounds__(kBlock) void embed_kernel(const uint8_t* __restrict__ table,
+                                                       const int* __restrict__ token, float* __restrict__ x,
+                                                       int n_vocab, int dim) {
     const int t = *token;
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= dim || t < 0 || t >= n_vocab) return;
     const int nb = dim / 32, b = i / 32, j = i % 32;
-    const uint8_t* blk = table + ((size_t)t * nb + b) * 18;
+    const uint8_t* blk = table + ((size_t)t * nb + b) * (kQ8 ? 34 : 18);
     const float d = __half2float(__ushort_as_half((unsigned short)(blk[0] | (blk[1] << 8))));
-    const int n = j < 16 ? (blk[2 + j] & 15) : (blk[2 + j - 16] >> 4);
-    x[i] = ((float)n - 8.0f) * d;
+    if (kQ8) {
+        x[i] = (float)(int8_t)blk[2 + j] * d;
+    } else {
+        const int n = j < 16 ? (blk[2 + j] & 15) : (blk[2 + j - 16] >> 4);
+        x[i] = ((float)n - 8.0f) * d;
+    }
 }
 
 // ---- greedy argmax (first index of the maximum, as numpy.argmax) -------------------------
@@ -529,17 +566,28 @@ int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* pa
             hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
                                n_heads, n_kv, pos_ptr, max_ctx, theta);
         hipLaunchKernelGGL((attn_decode_merge<64>), dim3(n_heads), dim3(64), 0, st, part, out, splits);
+    } else if (hd == 48) {
+        if (rope)
+            hipLaunchKernelGGL((attn_decode_kernel<48, true>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                               n_heads, n_kv, pos_ptr, max_ctx, theta);
+        else
+            hipLaunchKernelGGL((attn_decode_kernel<48, false>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                               n_heads, n_kv, pos_ptr, max_ctx, theta);
+        hipLaunchKernelGGL((attn_decode_merge<48>), dim3(n_heads), dim3(48), 0, st, part, out, splits);
     } else {
-        return fail(kUnsupported, "attention: head_dim %d (supported: 64, 128)", hd);
+        return fail(kUnsupported, "attention: head_dim %d (supported: 48, 64, 128)", hd);
     }
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }
 
-int embed_q4_0_launch(const void* table, const int* token, float* x, int n_vocab, int dim, hipStream_t st) {
+int embed_launch(QuantType qt, const void* table, const int* token, float* x, int n_vocab, int dim, hipStream_t st) {
     if (dim % 32) return fail(kInvalidArgument, "embedding: dim %% 32 != 0");
-    hipLaunchKernelGGL(embed_q4_0_kernel, dim3((dim + kBlock - 1) / kBlock), dim3(kBlock), 0, st,
-                       (const uint8_t*)table, token, x, n_vocab, dim);
+    const dim3 grid((dim + kBlock - 1) / kBlock);
+    if (qt == QuantType::Q8_0)
+        hipLaunchKernelGGL((embed_kernel<true>), grid, dim3(kBlock), 0, st, (const uint8_t*)table, token, x, n_vocab, dim);
+    else
+        hipLaunchKernelGGL((embed_kernel<false>), grid, dim3(kBlock), 0, st, (const uint8_t*)table, token, x, n_vocab, dim);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

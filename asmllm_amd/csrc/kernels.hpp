@@ -85,7 +85,8 @@ int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx);
 int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* part, float* out, int n_heads,
                        int n_kv, int hd, const int* pos_ptr, int max_ctx, bool rope, float theta, hipStream_t st);
 
-int embed_q4_0_launch(const void* table, const int* token, float* x, int n_vocab, int dim, hipStream_t st);
+// x = row *token of a Q4_0 or Q8_0 GGUF table [n_vocab][dim], exact.
+int embed_launch(QuantType qt, const void* table, const int* token, float* x, int n_vocab, int dim, hipStream_t st);
 int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st);
 
 }  // namespace asmhip

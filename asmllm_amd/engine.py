@@ -20,7 +20,10 @@ stream, so it can be captured once into a HIP graph and replayed per token:
   * RoPE and the KV-cache write are fused into the attention launch
     (asmhip_attention_decode_rope);
   * the KV cache is fp16, head-major [n_kv_heads][max_ctx][head_dim] per layer
-    (the reference keeps fp32 [128][heads][head_dim], generate.py:252-253).
+    (the reference keeps fp32 [128][heads][head_dim], generate.py:252-253);
+  * head_dim 48 (the reference's stories15M demo model, dim 288), 64 or 128;
+    where dim or hidden_dim is not a multiple of 64 the RMSNorm / SwiGLU runs
+    as its own launch before the matvec instead of inside it.
 
 All weights are Q4_0 GGUF blocks, including the token embedding and the
 lm-head (generate.py:182-184 loads both through get_tensor).
@@ -35,7 +38,7 @@ import numpy as np
 
 from . import native
 from .device import DeviceBuffer, Graph, Stream
-from .gguf import q4_0_nbytes
+from .gguf import q4_0_nbytes, q8_0_nbytes
 from .native import check
 
 
@@ -79,6 +82,9 @@ class LlamaShape:
 
 
 LLAMA_7B = LlamaShape()
+# The reference's end-to-end demo model (generate.py:122-164: stories15M, 6 layers,
+# dim 288, 6 heads of 48, FFN 768, vocab 32000, eps 1e-5).
+STORIES_15M = LlamaShape(dim=288, n_layers=6, n_heads=6, n_kv_heads=6, hidden_dim=768, vocab=32000, eps=1e-5)
 
 
 def shape_from_gguf(g) -> LlamaShape:
@@ -126,12 +132,15 @@ class DecodeEngine:
     blocks instead.
     """
 
-    def __init__(self, shape: LlamaShape = LLAMA_7B, max_ctx: int = 2176, stream: Stream | None = None):
+    def __init__(self, shape: LlamaShape = LLAMA_7B, max_ctx: int = 2176, stream: Stream | None = None,
+                 embed_type: int = native.Q4_0, output_type: int = native.Q4_0):
         s = shape
+        if embed_type not in (native.Q4_0, native.Q8_0) or output_type not in (native.Q4_0, native.Q8_0):
+            raise ValueError("the token embedding and the lm-head must be Q4_0 or Q8_0")
         if s.dim % s.n_heads or s.n_heads % s.n_kv_heads:
             raise ValueError("dim must split into heads, and heads into kv groups")
-        if s.head_dim not in (64, 128):
-            raise ValueError("head_dim must be 64 or 128")
+        if s.head_dim not in (48, 64, 128):
+            raise ValueError("head_dim must be 48, 64 or 128")
         if s.dim % 32 or s.hidden_dim % 32:
             raise ValueError("dim and hidden_dim must be multiples of 32 (Q4_0 blocks)")
         self.shape = s
@@ -139,15 +148,22 @@ class DecodeEngine:
         self.stream = stream or Stream()
         self.lib = native.lib()
         self.layers = [_Layer(s, self.max_ctx) for _ in range(s.n_layers)]
-        self.embed = DeviceBuffer(q4_0_nbytes(s.vocab, s.dim))
+        self.embed_type, self.output_type = embed_type, output_type
+        nbytes = {native.Q4_0: q4_0_nbytes, native.Q8_0: q8_0_nbytes}
+        self.embed = DeviceBuffer(nbytes[embed_type](s.vocab, s.dim))
         self.final_norm = DeviceBuffer(4 * s.dim)
-        self.output = DeviceBuffer(q4_0_nbytes(s.vocab, s.dim))
+        self.output = DeviceBuffer(nbytes[output_type](s.vocab, s.dim))
         # activations
         self.x = DeviceBuffer(4 * s.dim)
         self.qkv = DeviceBuffer(4 * s.qkv_rows)
         self.attn = DeviceBuffer(4 * s.dim)
         self.gu = DeviceBuffer(4 * 2 * s.hidden_dim)
         self.logits = DeviceBuffer(4 * s.vocab)
+        # The matvecs fuse RMSNorm / SwiGLU into their read of x when K % 64 == 0;
+        # otherwise (stories15M: dim 288) the op runs as its own launch first.
+        self.fuse_norm = s.dim % 64 == 0
+        self.fuse_swiglu = s.hidden_dim % 64 == 0
+        self.xn = None if self.fuse_norm else DeviceBuffer(4 * s.dim)
         ws = self.lib.asmhip_attention_decode_workspace(s.n_heads, s.head_dim, self.max_ctx)
         self.workspace = DeviceBuffer(4 * max(int(ws), 1))
         self.token = DeviceBuffer(4)
@@ -161,8 +177,8 @@ class DecodeEngine:
         s, L, st = self.shape, self.lib, self.stream.handle
         d, h = s.dim, s.hidden_dim
 
-        def blocks(buf, rows, K, tag):
-            check(L.asmhip_random_blocks(native.Q4_0, buf.ptr, rows, K, seed * 1000003 + tag, stddev, st),
+        def blocks(buf, rows, K, tag, qtype=native.Q4_0):
+            check(L.asmhip_random_blocks(qtype, buf.ptr, rows, K, seed * 1000003 + tag, stddev, st),
                   "random weights")
 
         for i, ly in enumerate(self.layers):
@@ -176,8 +192,8 @@ class DecodeEngine:
             n_kv = s.n_kv_heads * self.max_ctx * s.head_dim
             check(L.asmhip_random_f16(ly.k_cache.ptr, n_kv, seed * 1000003 + base + 4, kv_stddev, st), "kv")
             check(L.asmhip_random_f16(ly.v_cache.ptr, n_kv, seed * 1000003 + base + 5, kv_stddev, st), "kv")
-        blocks(self.embed, s.vocab, d, 1)
-        blocks(self.output, s.vocab, d, 2)
+        blocks(self.embed, s.vocab, d, 1, self.embed_type)
+        blocks(self.output, s.vocab, d, 2, self.output_type)
         check(L.asmhip_fill_f32(self.final_norm.ptr, d, 1.0, st), "norm weights")
         self.stream.synchronize()
 
@@ -193,6 +209,11 @@ class DecodeEngine:
         ly.wdown.upload(w_down)
 
     def load_globals(self, *, embed, final_norm, output) -> None:
+        """Token embedding and lm-head as host GGUF blocks of the engine's
+        embed_type / output_type, final norm weights fp32."""
+        for name, arr, buf in (("embedding", embed, self.embed), ("lm-head", output, self.output)):
+            if np.asarray(arr).nbytes != buf.nbytes:
+                raise ValueError(f"{name}: {np.asarray(arr).nbytes} bytes, the engine holds {buf.nbytes}")
         self.embed.upload(embed)
         self.final_norm.upload(np.asarray(final_norm, np.float32))
         self.output.upload(output)
@@ -201,15 +222,26 @@ class DecodeEngine:
     def from_gguf(cls, path, max_ctx: int = 2048, stream: Stream | None = None) -> "DecodeEngine":
         """Engine for a Llama GGUF model, every tensor uploaded once to HBM
         (the tensor names of generate.py:182-205; the shape from the llama.*
-        metadata).  Linear weights and the token embedding must be Q4_0, norm
-        weights F32; a model without output.weight uses the token embedding
+        metadata).  Layer weights must be Q4_0; the token embedding and the
+        lm-head Q4_0 or Q8_0 (generate.py:169-180 reads both types); norm
+        weights F32.  A model without output.weight uses the token embedding
         as its lm-head."""
-        from .gguf_file import F32, Q4_0, GGUFFile
+        from .gguf_file import F32, Q4_0, Q8_0, GGUFFile
 
         g = GGUFFile(path)
         try:
             shape = shape_from_gguf(g)
-            eng = cls(shape, max_ctx=max_ctx, stream=stream)
+            out_name = "output.weight" if "output.weight" in g.tensors else "token_embd.weight"
+            types = {}
+            for name in ("token_embd.weight", out_name):
+                t = g.tensors.get(name)
+                if t is None:
+                    raise KeyError(f"{path}: no tensor {name!r}")
+                if t.type not in (Q4_0, Q8_0):
+                    raise ValueError(f"{name}: tensor type {t.type}; the engine takes Q4_0 ({Q4_0}) or Q8_0 ({Q8_0})")
+                types[name] = native.Q4_0 if t.type == Q4_0 else native.Q8_0
+            eng = cls(shape, max_ctx=max_ctx, stream=stream, embed_type=types["token_embd.weight"],
+                      output_type=types[out_name])
 
             def q4(name):
                 t = g.tensors.get(name)
@@ -231,9 +263,8 @@ class DecodeEngine:
                                wk=q4(b + "attn_k.weight"), wv=q4(b + "attn_v.weight"), wo=q4(b + "attn_output.weight"),
                                ffn_norm=f32(b + "ffn_norm.weight"), w_gate=q4(b + "ffn_gate.weight"),
                                w_up=q4(b + "ffn_up.weight"), w_down=q4(b + "ffn_down.weight"))
-            embed = q4("token_embd.weight")
-            output = q4("output.weight") if "output.weight" in g.tensors else embed
-            eng.load_globals(embed=embed, final_norm=f32("output_norm.weight"), output=output)
+            eng.load_globals(embed=g.tensor("token_embd.weight"), final_norm=f32("output_norm.weight"),
+                             output=g.tensor(out_name))
             eng.vocab = g.vocab()
         finally:
             g.close()
@@ -259,19 +290,31 @@ class DecodeEngine:
         eps = ctypes.c_float(s.eps)
         Q4, RMS, SWI, NONE = native.Q4_0, native.PRE_RMSNORM, native.PRE_SWIGLU, native.PRE_NONE
 
-        def mv(w, x, y, M, K, pre, arg, acc, what):
-            check(L.asmhip_matmul_fused(Q4, w.ptr, x.ptr, y, M, K, pre, arg, eps, acc, st), what)
+        def mv(w, x, y, M, K, pre, arg, acc, what, qtype=Q4):
+            check(L.asmhip_matmul_fused(qtype, w.ptr, x, y, M, K, pre, arg, eps, acc, st), what)
 
-        check(L.asmhip_embed_q4_0(self.embed.ptr, self.token.ptr, self.x.ptr, s.vocab, d, st), "embed")
+        def normed(norm, M, w, y, what, qtype=Q4):  # y = W rmsnorm(x; norm)
+            if self.fuse_norm:
+                mv(w, self.x.ptr, y, M, d, RMS, norm.ptr, 0, what, qtype)
+            else:
+                check(L.asmhip_rmsnorm(self.x.ptr, norm.ptr, self.xn.ptr, d, eps, st), "rmsnorm")
+                mv(w, self.xn.ptr, y, M, d, NONE, None, 0, what, qtype)
+
+        embed = L.asmhip_embed_q8_0 if self.embed_type == native.Q8_0 else L.asmhip_embed_q4_0
+        check(embed(self.embed.ptr, self.token.ptr, self.x.ptr, s.vocab, d, st), "embed")
         for ly in self.layers:
-            mv(ly.wqkv, self.x, self.qkv.ptr, s.qkv_rows, d, RMS, ly.attn_norm.ptr, 0, "qkv matvec")
+            normed(ly.attn_norm, s.qkv_rows, ly.wqkv, self.qkv.ptr, "qkv matvec")
             check(L.asmhip_attention_decode_rope(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr, self.workspace.ptr,
                                                  self.attn.ptr, s.n_heads, s.n_kv_heads, hd, self.pos.ptr,
                                                  self.max_ctx, ctypes.c_float(s.theta), st), "rope + attention")
-            mv(ly.wo, self.attn, self.x.ptr, d, d, NONE, None, 1, "o matvec")
-            mv(ly.wgu, self.x, self.gu.ptr, 2 * h, d, RMS, ly.ffn_norm.ptr, 0, "gate/up matvec")
-            mv(ly.wdown, self.gu, self.x.ptr, d, h, SWI, self.gu.ptr + 4 * h, 1, "down matvec")
-        mv(self.output, self.x, self.logits.ptr, s.vocab, d, RMS, self.final_norm.ptr, 0, "lm-head matvec")
+            mv(ly.wo, self.attn.ptr, self.x.ptr, d, d, NONE, None, 1, "o matvec")
+            normed(ly.ffn_norm, 2 * h, ly.wgu, self.gu.ptr, "gate/up matvec")
+            if self.fuse_swiglu:
+                mv(ly.wdown, self.gu.ptr, self.x.ptr, d, h, SWI, self.gu.ptr + 4 * h, 1, "down matvec")
+            else:
+                check(L.asmhip_silu_hadamard(self.gu.ptr, self.gu.ptr + 4 * h, h, st), "silu * up")
+                mv(ly.wdown, self.gu.ptr, self.x.ptr, d, h, NONE, None, 1, "down matvec")
+        normed(self.final_norm, s.vocab, self.output, self.logits.ptr, "lm-head matvec", self.output_type)
         check(L.asmhip_argmax(self.logits.ptr, s.vocab, self.token.ptr, self.pos.ptr, st), "argmax")
 
     def set_position(self, token_id: int, pos: int) -> None:

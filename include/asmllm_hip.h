@@ -199,7 +199,7 @@ ASMHIP_API int asmhip_attention(const float* q, const float* k, const float* v, 
  * n_kv_heads)), softmax(q_h . k_p / sqrt(head_dim)) . v_p over positions
  * 0..*pos_dev (max_ctx <= 8192); workspace holds
  * asmhip_attention_decode_workspace() floats (calls sharing one workspace
- * must not overlap).  head_dim 64 or 128. */
+ * must not overlap).  head_dim 48, 64 or 128. */
 ASMHIP_API int asmhip_rope_kv_write(float* qkv, void* k_cache, void* v_cache, int n_heads, int n_kv_heads,
                                     int head_dim, const int* pos_dev, int max_ctx, float theta, void* stream);
 ASMHIP_API int64_t asmhip_attention_decode_workspace(int n_heads, int head_dim, int max_ctx);
@@ -215,6 +215,9 @@ ASMHIP_API int asmhip_attention_decode_rope(const float* qkv, void* k_cache, voi
 /* x = row *token_dev of a Q4_0 embedding table [n_vocab][dim]
  * (generate.py:262, the table dequantized by get_tensor :169-182). */
 ASMHIP_API int asmhip_embed_q4_0(const void* table, const int* token_dev, float* x, int n_vocab, int dim,
+                                 void* stream);
+/* The same for a Q8_0 table (generate.py:169-182 also dequantizes type 8). */
+ASMHIP_API int asmhip_embed_q8_0(const void* table, const int* token_dev, float* x, int n_vocab, int dim,
                                  void* stream);
 /* *token_dev = first index of max(logits) (numpy.argmax, generate.py:419-420);
  * then ++*pos_dev when pos_dev is not NULL. */

@@ -24,7 +24,8 @@ from . import native as o
 
 
 class DecodeRef:
-    """Host copy of a decode model: GGUF Q4_0 blocks ([rows][K/32][18] uint8),
+    """Host copy of a decode model: GGUF Q4_0 blocks ([rows][K/32][18] uint8;
+    the embedding and lm-head may be Q8_0, [rows][K/32][34]),
     fp32 norm weights, fp16 caches given head-major [n_kv][max_ctx][hd] as
     uint16 bits (stored position-major in k_caches / v_caches)."""
 
@@ -42,6 +43,8 @@ class DecodeRef:
         self.nt = nt
 
     def _mv(self, blocks, x):
+        if blocks.shape[-1] == 34:  # Q8_0 blocks (an lm-head; generate.py:177-180)
+            return o.matmul_q8_0_gguf(blocks, x, self.nt)
         return o.matmul_q4_0_gguf(blocks, x, self.nt)
 
     def _rope_heads(self, v, n):
@@ -55,7 +58,8 @@ class DecodeRef:
         """Logits of token_id at pos; writes cache row pos (generate.py:261-326)."""
         self._pos = pos
         hd, nh, nkv = self.hd, self.n_heads, self.n_kv_heads
-        x = o.dequantize_q4_0(self.embed[token_id:token_id + 1])[0].copy()        # :262
+        row = self.embed[token_id:token_id + 1]
+        x = (o.dequantize_q8_0(row) if row.shape[-1] == 34 else o.dequantize_q4_0(row))[0].copy()  # :262
         for li, ly in enumerate(self.layers):
             xn = o.rmsnorm(x, ly["attn_norm"], self.eps)                          # :268-272
             q = self._mv(ly["wq"], xn)                                            # :278-280

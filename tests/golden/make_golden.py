@@ -9,6 +9,9 @@ quant_known_answers.npz: hand-constructed Q4_0 / Q8_0 blocks whose bytes
 follow from the quantization rule by hand; the expected bytes below are
 literals, not recomputed.
 
+stories15m_m2_tokens.json: the prompt and greedy tokens of the reference's
+end-to-end stories15M run, read from its log (tests/results/m2_generation.log).
+
 Run: python tests/golden/make_golden.py
 """
 
@@ -81,11 +84,31 @@ def quant_known_answers() -> dict[str, np.ndarray]:
     return {"q4_w": q4_w, "q4_blocks": q4_blocks, "q8_w": q8_w, "q8_blocks": q8_blocks}
 
 
+M2_LOG = Path("/root/reference/tests/results/m2_generation.log")
+
+
+def m2_tokens(log_text: str) -> dict:
+    """The prompt and the 30 greedy token ids of the reference's end-to-end
+    run on stories15M (m2_generation.log:5, 10-39), read from the log's text."""
+    import re
+
+    prompt = [int(t) for t in re.search(r"Prompt Tokens: \[([\d, ]+)\]", log_text).group(1).split(",")]
+    rows = re.findall(r"^(\d+)\s+(\d+)\s+'.*?'\s+(\d+)\s+(\w+)", log_text, re.M)
+    assert [int(r[0]) for r in rows] == list(range(1, len(rows) + 1))
+    assert all(r[1] == r[2] and r[3] == "YES" for r in rows)  # the reference's own check passed
+    return {"source": "tests/results/m2_generation.log (asmllm), stories15M-q4_0.gguf greedy decode",
+            "prompt": prompt, "generated": [int(r[1]) for r in rows]}
+
+
 def main() -> None:
+    import json
+
     data = generate_reference_data(42)
     np.savez_compressed(HERE / "reference_gen_seed42.npz", **data)
     np.savez_compressed(HERE / "quant_known_answers.npz", **quant_known_answers())
-    print("wrote", sorted(p.name for p in HERE.glob("*.npz")))
+    if M2_LOG.exists():  # the reference tree is only present where the fixtures are made
+        (HERE / "stories15m_m2_tokens.json").write_text(json.dumps(m2_tokens(M2_LOG.read_text()), indent=1) + "\n")
+    print("wrote", sorted(p.name for p in HERE.glob("*.npz")) + sorted(p.name for p in HERE.glob("*.json")))
 
 
 if __name__ == "__main__":

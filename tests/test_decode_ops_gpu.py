@@ -121,6 +121,8 @@ def test_multi_head_rope_reads_position_on_device(hip, oracle):
 @pytest.mark.parametrize("n_heads,n_kv,hd,pos,max_ctx", [
     (32, 32, 128, 0, 256), (32, 32, 128, 2047, 2176), (32, 8, 128, 700, 1024), (8, 2, 64, 129, 130),
     (32, 8, 128, 128, 300), (4, 4, 128, 127, 128), (8, 8, 64, 8191, 8192),
+    # head_dim 48 (stories15M): one split, several, and 64 splits (more than the merge's 48 threads)
+    (6, 6, 48, 5, 64), (6, 6, 48, 300, 2048), (6, 2, 48, 8000, 8192),
 ])
 def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos, max_ctx):
     rng = np.random.default_rng(n_heads * 1000 + pos)
@@ -185,6 +187,11 @@ def test_embed_row_and_argmax(hip, oracle):
     _ok(hip, hip.asmhip_embed_q4_0(dt.ptr, dtok.ptr, dx.ptr, n_vocab, dim, None))
     synchronize()
     np.testing.assert_array_equal(dx.download(np.float32, dim), oracle.dequantize_q4_0(table[417:418])[0])
+    t8 = gguf.quantize_q8_0(rng.standard_normal((n_vocab, 288)).astype(np.float32))
+    dt8, dx8 = DeviceBuffer.from_numpy(t8), DeviceBuffer(288 * 4)
+    _ok(hip, hip.asmhip_embed_q8_0(dt8.ptr, dtok.ptr, dx8.ptr, n_vocab, 288, None))
+    synchronize()
+    np.testing.assert_array_equal(dx8.download(np.float32, 288), oracle.dequantize_q8_0(t8[417:418])[0])
 
     logits = rng.standard_normal(32000).astype(np.float32)
     logits[[123, 31000]] = 9.0  # tie: the first index wins, as numpy.argmax

@@ -11,15 +11,16 @@ the eager launches bit for bit.
 import numpy as np
 import pytest
 
-from asmllm_amd.engine import LLAMA_7B, DecodeEngine, LlamaShape
+from asmllm_amd import native
+from asmllm_amd.engine import LLAMA_7B, STORIES_15M, DecodeEngine, LlamaShape
 from asmllm_amd.gguf import q4_0_nbytes
 
 pytestmark = pytest.mark.gpu
 LOGIT_TOL = 2e-4
 
 
-def _blocks(buf, rows, K):
-    return buf.download(np.uint8, (rows, K // 32, 18))
+def _blocks(buf, rows, K, qtype=native.Q4_0):
+    return buf.download(np.uint8, (rows, K // 32, 34 if qtype == native.Q8_0 else 18))
 
 
 def _oracle_model(eng: DecodeEngine, nt: int):
@@ -40,8 +41,9 @@ def _oracle_model(eng: DecodeEngine, nt: int):
         kcs.append(ly.k_cache.download(np.uint16, shape))
         vcs.append(ly.v_cache.download(np.uint16, shape))
     return DecodeRef(dim=d, n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, hidden_dim=h, vocab=s.vocab, eps=s.eps,
-                     theta=s.theta, embed=_blocks(eng.embed, s.vocab, d),
-                     final_norm=eng.final_norm.download(np.float32, d), output=_blocks(eng.output, s.vocab, d),
+                     theta=s.theta, embed=_blocks(eng.embed, s.vocab, d, eng.embed_type),
+                     final_norm=eng.final_norm.download(np.float32, d),
+                     output=_blocks(eng.output, s.vocab, d, eng.output_type),
                      layers=layers, k_caches=kcs, v_caches=vcs, nt=nt)
 
 
@@ -60,11 +62,17 @@ SMALL = [
     LlamaShape(dim=512, n_layers=2, n_heads=4, n_kv_heads=2, hidden_dim=1408, vocab=777, eps=1e-5),
     LlamaShape(dim=512, n_layers=3, n_heads=8, n_kv_heads=8, hidden_dim=1024, vocab=4096, theta=5e5),
 ]
+# (shape, embedding type, lm-head type): the stories15M shape (head_dim 48, dim 288: RMSNorm not
+# fused) with a Q8_0 lm-head, and a Q8_0 embedding at a fused shape.
+CASES = [(SMALL[0], native.Q4_0, native.Q4_0), (SMALL[1], native.Q4_0, native.Q4_0),
+         (SMALL[2], native.Q4_0, native.Q4_0), (STORIES_15M, native.Q4_0, native.Q8_0),
+         (SMALL[1], native.Q8_0, native.Q8_0)]
 
 
-@pytest.mark.parametrize("shape", SMALL, ids=["mha", "gqa", "hd64"])
-def test_decode_steps_match_oracle(shape):
-    eng = DecodeEngine(shape, max_ctx=48)
+@pytest.mark.parametrize("shape,embed_type,output_type", CASES,
+                         ids=["mha", "gqa", "hd64", "stories15m_q8_head", "q8_embed_head"])
+def test_decode_steps_match_oracle(shape, embed_type, output_type):
+    eng = DecodeEngine(shape, max_ctx=48, embed_type=embed_type, output_type=output_type)
     eng.init_random(seed=7)
     ref = _oracle_model(eng, nt=4)
     token, pos0 = 5, 29
@@ -126,7 +134,7 @@ def test_7b_shape_step_at_context_2048_matches_oracle():
     eng.close()
 
 
-def _write_llama_gguf(path, s: LlamaShape, seed: int, tied: bool):
+def _write_llama_gguf(path, s: LlamaShape, seed: int, tied: bool, output_q8: bool = False):
     from asmllm_amd import gguf
     from asmllm_amd import gguf_file as gf
 
@@ -139,7 +147,11 @@ def _write_llama_gguf(path, s: LlamaShape, seed: int, tied: bool):
     t = {"token_embd.weight": (gf.Q4_0, (d, s.vocab), q4(s.vocab, d)),
          "output_norm.weight": (gf.F32, (d,), rng.uniform(0.5, 1.5, d).astype(np.float32))}
     if not tied:
-        t["output.weight"] = (gf.Q4_0, (d, s.vocab), q4(s.vocab, d))
+        if output_q8:
+            w = gguf.quantize_q8_0((rng.standard_normal((s.vocab, d)) * 0.05).astype(np.float32))
+            t["output.weight"] = (gf.Q8_0, (d, s.vocab), w)
+        else:
+            t["output.weight"] = (gf.Q4_0, (d, s.vocab), q4(s.vocab, d))
     for i in range(s.n_layers):
         b = f"blk.{i}."
         t[b + "attn_norm.weight"] = (gf.F32, (d,), rng.uniform(0.5, 1.5, d).astype(np.float32))
@@ -157,17 +169,22 @@ def _write_llama_gguf(path, s: LlamaShape, seed: int, tied: bool):
     gf.write_gguf(path, meta, t, alignment=64)
 
 
-@pytest.mark.parametrize("tied", [False, True], ids=["lm_head", "tied_embedding"])
-def test_engine_from_gguf_matches_oracle(tmp_path, tied):
+TINY = LlamaShape(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, hidden_dim=512, vocab=500,
+                  eps=float(np.float32(1e-5)))  # as the file stores it
+STORIES_FILE = LlamaShape(**{**STORIES_15M.__dict__, "eps": float(np.float32(1e-5))})
+
+
+@pytest.mark.parametrize("s,tied,output_q8", [(TINY, False, False), (TINY, True, False), (STORIES_FILE, False, True)],
+                         ids=["lm_head", "tied_embedding", "stories15m_shape_q8_head"])
+def test_engine_from_gguf_matches_oracle(tmp_path, s, tied, output_q8):
     """A GGUF Llama (generate.py:182-205 tensor names) loaded once into HBM
-    decodes as the oracle's forward_token on the file's own tensors."""
+    decodes as the oracle's forward_token on the file's own tensors; the last
+    case has the reference demo model's architecture (synthetic weights)."""
     from asmllm_amd import gguf_file as gf
     from oracle.decode_ref import DecodeRef
 
-    s = LlamaShape(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, hidden_dim=512, vocab=500,
-                   eps=float(np.float32(1e-5)))  # as the file stores it
     path = tmp_path / "tiny.gguf"
-    _write_llama_gguf(path, s, seed=11, tied=tied)
+    _write_llama_gguf(path, s, seed=11, tied=tied, output_q8=output_q8)
     max_ctx = 32
     eng = DecodeEngine.from_gguf(path, max_ctx=max_ctx)
     assert eng.shape == s and eng.vocab[:2] == ["t0", "t1"]
@@ -191,4 +208,41 @@ def test_engine_from_gguf_matches_oracle(tmp_path, tied):
         want = ref.forward_token(token, pos)
         _check_logits(got, want, f"pos {pos}")
         token = int(np.argmax(want))
+    eng.close()
+
+
+M2_FIXTURE = "stories15m_m2_tokens.json"
+
+
+def _stories15m_path():
+    import os
+    from pathlib import Path
+
+    for cand in (os.environ.get("ASMLLM_STORIES15M", ""), "models/stories15M-q4_0.gguf", "stories15M-q4_0.gguf"):
+        if cand and Path(cand).is_file() and Path(cand).stat().st_size >= 1024:
+            return Path(cand)
+    return None
+
+
+def test_stories15m_greedy_matches_reference_log():
+    """The reference's end-to-end check (generate.py:382-430): prompt
+    [1, 9038, 2501, 263, 931] fed token by token, then 30 greedy tokens, which
+    must equal the tokens in the reference's own log (m2_generation.log:10-39,
+    kept in tests/golden).  Needs the published stories15M-q4_0.gguf, which
+    is not available offline: set ASMLLM_STORIES15M or place it in models/."""
+    import json
+
+    from conftest import GOLDEN_DIR
+
+    path = _stories15m_path()
+    if path is None:
+        pytest.skip("stories15M-q4_0.gguf not present (no network to fetch it)")
+    want = json.loads((GOLDEN_DIR / M2_FIXTURE).read_text())
+    eng = DecodeEngine.from_gguf(path, max_ctx=64)
+    assert eng.shape.dim == 288 and eng.shape.head_dim == 48
+    prompt = want["prompt"]
+    for pos, tok in enumerate(prompt[:-1]):
+        eng.forward_token(tok, pos)
+    got = eng.generate(prompt[-1], len(prompt) - 1, len(want["generated"]), use_graph=True)
+    assert got == want["generated"]
     eng.close()
