@@ -48,6 +48,9 @@ int get_q4_kernel();
 bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& opts, int64_t M, int64_t K);
 int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t stream,
                      const MatvecOpts& opts);
+// The same stream over 22-byte GGUF Q5_0 blocks (no fused pre-ops).
+bool q5_0_mfma_eligible(const void* w, const float* x, int64_t M, int64_t K);
+int q5_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t stream);
 
 // C[T][M] = A (Q8_0 blocks [T][K/32]) x W (Q8_0 blocks [M][K/32])^T, block dots
 // scaled by both fp16 scales and accumulated in block order.

@@ -744,6 +744,7 @@ int q5_matvec_launch(bool gguf, const void* w, const uint8_t* qh, const float* s
     const bool pairs = nb % 2 == 0 && aligned && lds <= 160 * 1024 - 256 && total < (int64_t)UINT32_MAX;
     const int m = (int)M, k = (int)K;
     int rc = kOk;
+    if (gguf && q5_0_mfma_eligible(w, x, M, K)) return q5_0_mfma_launch(w, x, y, M, K, stream);
     if (pairs) {
         const int r = pick_rows_per_wave(M, 4);
         if (gguf) {

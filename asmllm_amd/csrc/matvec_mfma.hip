@@ -56,14 +56,35 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kUnitBlocks = 8;                     // blocks per unit
-constexpr int kUnitRowBytes = kUnitBlocks * 18;    // 144: one row's slice of a unit
-constexpr int kUnitBytes = 16 * kUnitRowBytes;     // 2304 bytes of weights per unit
-constexpr int kUnitPieces = kUnitBytes / 16;       // 144 16-byte pieces: 3 loads per lane
-constexpr int kRowPitch = 152;                     // LDS bytes per staged row: 38 dwords, so the
-                                                   // operand reads of 16 rows x 2 lane groups hit
-                                                   // 32 distinct banks (a 144-byte pitch pairs rows
-                                                   // n and n + 8 on one bank)
-constexpr int kSlotBytes = 16 * kRowPitch;         // 2432: LDS slot per wave
+
+// GGUF block formats the stream reads in place.  A unit is 16 rows x 8 blocks;
+// each row's slice is parked in LDS at a padded pitch.
+enum BlockFmt : int { kFmtQ4_0 = 0, kFmtQ5_0 = 1 };
+template <int QT>
+struct Fmt;
+template <>
+struct Fmt<kFmtQ4_0> {
+    static constexpr int kBlockBytes = 18;   // fp16 d, qs[16]
+    static constexpr int kRowPitch = 152;    // 38 dwords: the operand reads of 16 rows hit distinct
+                                             // banks (a 144-byte pitch pairs rows n and n + 8)
+    static constexpr int kXScaleShift = 34;  // weight bytes hold 16 (n - 8): x scale 2^(e - 30) / 16
+};
+template <>
+struct Fmt<kFmtQ5_0> {
+    static constexpr int kBlockBytes = 22;   // fp16 d, qh[4], qs[16]
+    static constexpr int kRowPitch = 184;    // 46 dwords: 16 rows on 16 distinct even banks
+    static constexpr int kXScaleShift = 33;  // weight bytes hold 8 (b - 16): x scale 2^(e - 30) / 8
+};
+template <int QT>
+struct Unit {
+    static constexpr int kBB = Fmt<QT>::kBlockBytes;
+    static constexpr int kRowBytes = kUnitBlocks * kBB;  // 144 / 176: one row's slice of a unit
+    static constexpr int kCols = kBB / 2;                // 16-byte pieces per row slice (9 / 11)
+    static constexpr int kPieces = 16 * kCols;           // 144 / 176: three 16-byte loads per lane
+    static constexpr int kPitch = Fmt<QT>::kRowPitch;
+    static constexpr int kSlotBytes = 16 * kPitch;       // LDS slot per wave
+    static_assert(kPieces <= 3 * 64, "a unit is three 16-byte loads per lane");
+};
 constexpr int kXStride = 272;                      // LDS bytes of x digits per block: [half][level*4+digit][16] + 16 pad
                                                    // (16-byte rows for the 16-byte A operands)
                                                    // (the pad staggers blocks across banks: conflict-free 8-byte writes)
@@ -71,13 +92,13 @@ constexpr int kMaxBlocks = 512;                    // K <= 16384
 constexpr int kMaxTilesPerGroup = 8;
 constexpr uint32_t kPastEnd = 0xFFFFFF00u;         // buffer offset that loads zeros
 
-static_assert(kUnitPieces <= 3 * 64, "a unit is three 16-byte loads per lane");
-
-// Piece q of a unit (row q / 9, bytes 16 (q % 9) of its 144-byte slice) into
+// Piece q of a unit (row q / kCols, bytes 16 (q % kCols) of its slice) into
 // the wave's LDS slot at the padded row pitch (8-byte aligned: two b64 stores).
+template <int QT>
 __device__ __forceinline__ void park_piece(uint8_t* wbuf, int q, uint4 v) {
-    const int r = q / 9, c = q - 9 * r;
-    uint2* dst = reinterpret_cast<uint2*>(wbuf + r * kRowPitch + 16 * c);
+    constexpr int C = Unit<QT>::kCols;
+    const int r = q / C, c = q - C * r;
+    uint2* dst = reinterpret_cast<uint2*>(wbuf + r * Unit<QT>::kPitch + 16 * c);
     dst[0] = make_uint2(v.x, v.y);
     dst[1] = make_uint2(v.z, v.w);
 }
@@ -124,45 +145,71 @@ __device__ __forceinline__ float block_value(v4i d) {
 // the level 1 / level 2 digit dots of block 2p and lanes 32-47 / 48-63 those
 // of block 2p + 1: every lane's epilogue is useful work.
 struct PairLane {
-    int bp;       // 0: this lane's block is the even one of the pair, 1: the odd one
-    int qoff;     // byte offset (dword aligned) of the lane's qs bytes in the pair's 36 bytes
-    uint32_t sh;  // alignbyte shift: 2 for the even block (qs two bytes off the dword grid), 0 for the odd
-    int doff;     // byte offset of the dword holding the block's fp16 scale
-    uint32_t dsh; // shift of that scale inside the dword
+    int bp;        // 0: this lane's block is the even one of the pair, 1: the odd one
+    int h;         // which 8 positions of each half of the block: 8h..8h+7, 16+8h..16+8h+7
+    int qoff;      // byte offset (dword aligned) of the lane's qs bytes within the pair
+    uint32_t sh;   // alignbyte shift: 2 where the block's fields sit two bytes off the dword grid
+    int hoff;      // Q5_0: byte offset (dword aligned) of the block's qh word
+    int doff;      // byte offset of the dword holding the block's fp16 scale
+    uint32_t dsh;  // shift of that scale inside the dword
 };
 
+template <int QT>
 __device__ __forceinline__ PairLane pair_lane(int lane) {
+    constexpr int BB = Fmt<QT>::kBlockBytes;
     const int G = lane >> 4, bp = G >> 1, h = G & 1;
+    const int o = BB * bp;                  // the block's first byte within the pair
+    const int qs = o + (BB - 16) + 8 * h;   // the lane's first qs byte
     PairLane pl;
     pl.bp = bp;
-    pl.qoff = bp ? 20 + 8 * h : 8 * h;  // (2 + 8h) & ~3 for the even block, 20 + 8h for the odd
-    pl.sh = bp ? 0u : 2u;
-    pl.doff = 16 * bp;
-    pl.dsh = 16u * (uint32_t)bp;
+    pl.h = h;
+    pl.qoff = qs & ~3;
+    pl.sh = (uint32_t)(qs & 3);
+    pl.hoff = (o + 2) & ~3;                 // qh at byte 2 of a Q5_0 block (same shift as qs)
+    pl.doff = o & ~3;
+    pl.dsh = 8u * (uint32_t)(o & 3);
     return pl;
+}
+
+// Q5_0 weight bytes 8 (b - 16) of four positions: the nibbles v (already at
+// bits 3..6 of each byte) with the inverted fifth bits nh[pos0 .. pos0+3] at
+// bit 7.  ((t << 7) * (1 + 2^7 + 2^14 + 2^21) puts bit j of the 4-bit t at
+// 8j + 7; the shifted copies do not overlap and both factors fit 24 bits.)
+__device__ __forceinline__ uint32_t q5_bytes(uint32_t nib3, uint32_t nh, int pos0) {
+    const uint32_t t = __builtin_amdgcn_ubfe(nh, (uint32_t)pos0, 4u) << 7;
+    return (nib3 & 0x78787878u) | (__umul24(t, 0x204081u) & 0x80808080u);
 }
 
 // Row n's dot with x over NB staged blocks (NB even), given the lane's A
 // operands aq[p] and block x-scales xs[p] (of the lane's block of pair p):
 // every weight operand is read from LDS first, then the MFMAs issue back to
 // back, then the per-pair epilogues.
-template <int NB>
+template <int NB, int QT>
 __device__ __forceinline__ float chunk_dot_x(const uint8_t* rowd, const PairLane& pl, const v4i* aq,
                                              const float* xs, float acc) {
-    constexpr int NP = NB / 2;
+    constexpr int NP = NB / 2, PB = 2 * Fmt<QT>::kBlockBytes;
     v4i bq[NP];
     uint32_t sc[NP];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-        const uint8_t* q = rowd + 36 * p + pl.qoff;
-        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(q);
-        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(q + 4);
-        const uint32_t w2 = *reinterpret_cast<const uint32_t*>(q + 8);
-        const uint32_t qa = __builtin_amdgcn_alignbyte(w1, w0, pl.sh);
-        const uint32_t qb = __builtin_amdgcn_alignbyte(w2, w1, pl.sh);
-        const long la = pack_q4(qa), lb = pack_q4(qb);  // (lo | hi << 32) of each dword
-        bq[p] = (v4i){(int)(uint32_t)la, (int)(uint32_t)lb, (int)(uint32_t)(la >> 32), (int)(uint32_t)(lb >> 32)};
-        sc[p] = *reinterpret_cast<const uint32_t*>(rowd + 36 * p + pl.doff) >> pl.dsh;
+        const uint8_t* pr = rowd + PB * p;
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(pr + pl.qoff);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(pr + pl.qoff + 4);
+        const uint32_t w2 = *reinterpret_cast<const uint32_t*>(pr + pl.qoff + 8);
+        const uint32_t qa = __builtin_amdgcn_alignbyte(w1, w0, pl.sh);  // qs bytes 8h..8h+3
+        const uint32_t qb = __builtin_amdgcn_alignbyte(w2, w1, pl.sh);  // qs bytes 8h+4..8h+7
+        if constexpr (QT == kFmtQ4_0) {
+            const long la = pack_q4(qa), lb = pack_q4(qb);  // (lo | hi << 32) of each dword
+            bq[p] = (v4i){(int)(uint32_t)la, (int)(uint32_t)lb, (int)(uint32_t)(la >> 32), (int)(uint32_t)(lb >> 32)};
+        } else {
+            const uint32_t h0 = *reinterpret_cast<const uint32_t*>(pr + pl.hoff);
+            const uint32_t h1 = *reinterpret_cast<const uint32_t*>(pr + pl.hoff + 4);
+            const uint32_t nh = ~__builtin_amdgcn_alignbyte(h1, h0, pl.sh);
+            const int b0 = 8 * pl.h;
+            bq[p] = (v4i){(int)q5_bytes(qa << 3, nh, b0), (int)q5_bytes(qb << 3, nh, b0 + 4),
+                          (int)q5_bytes(qa >> 1, nh, 16 + b0), (int)q5_bytes(qb >> 1, nh, 20 + b0)};
+        }
+        sc[p] = *reinterpret_cast<const uint32_t*>(pr + pl.doff) >> pl.dsh;
     }
     const v4i z = {0, 0, 0, 0};
     v4i d[NP];
@@ -182,7 +229,7 @@ __device__ __forceinline__ int a_offset(int lane) {
 }
 
 // The same with the A operands read from the x digits in LDS.
-template <int NB>
+template <int NB, int QT>
 __device__ __forceinline__ float chunk_dot(const uint8_t* rowd, const PairLane& pl, const uint8_t* xu, int aoff,
                                            const float* xsu, float acc) {
     constexpr int NP = NB / 2;
@@ -193,7 +240,7 @@ __device__ __forceinline__ float chunk_dot(const uint8_t* rowd, const PairLane& 
         aq[p] = aoff >= 0 ? *reinterpret_cast<const v4i*>(xu + 2 * p * kXStride + aoff) : (v4i){0, 0, 0, 0};
         xs[p] = xsu[2 * p + pl.bp];
     }
-    return chunk_dot_x<NB>(rowd, pl, aq, xs, acc);
+    return chunk_dot_x<NB, QT>(rowd, pl, aq, xs, acc);
 }
 
 // Row n's total from the lanes of a finished tile: level 1 + level 2 * 2^-30
@@ -206,17 +253,18 @@ __device__ __forceinline__ float tile_total(float acc) {
 // PW > 0: every wave streams exactly PW units of each tile (K = 256 NW PW), so
 // its x operands are the same for every tile and stay in registers; PW = 0:
 // any K, operands read from LDS per unit.
-template <int XQ, int NW, int D, int PW>
-__global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __restrict__ w,
+template <int QT, int XQ, int NW, int D, int PW>
+__global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int M, int K, int pre, const float* __restrict__ pre_arg,
                                                             float eps, int accumulate) {
+    using U = Unit<QT>;
     constexpr int kThreads = NW * 64;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ float red[NW];
     const int nb = K >> 5;
     const int nu = nb / kUnitBlocks;  // units per tile
-    const uint32_t row_bytes = (uint32_t)nb * 18u;
+    const uint32_t row_bytes = (uint32_t)nb * (uint32_t)U::kBB;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int G = gridDim.x;
     const int n_tiles = (M + 15) >> 4;
@@ -224,25 +272,25 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
     const int per_w = wave < nu ? (nu - wave + NW - 1) / NW : 0;  // this wave's units per tile
     const int L = my_tiles * per_w;                              // length of this wave's stream
     const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
-    uint8_t* wbuf = lds + wave * kSlotBytes;
-    uint8_t* xdig = lds + NW * kSlotBytes;
+    uint8_t* wbuf = lds + wave * U::kSlotBytes;
+    uint8_t* xdig = lds + NW * U::kSlotBytes;
     float* xscale = reinterpret_cast<float*>(xdig + nb * kXStride);
     float* part = xscale + nb;  // [my_tiles][NW][16]
 
-    // This lane's three 16-byte pieces of a unit: piece q = row q / 9, bytes
-    // 16 (q % 9) of the row's 144-byte slice.  Rows past M fall beyond the
+    // This lane's three 16-byte pieces of a unit: piece q = row q / kCols,
+    // bytes 16 (q % kCols) of the row's slice.  Rows past M fall beyond the
     // buffer and load zeros.
     uint32_t poff[3];
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-        const int q = min(lane + 64 * k, kUnitPieces - 1);
-        poff[k] = (uint32_t)(q / 9) * row_bytes + 16u * (uint32_t)(q % 9);
+        const int q = min(lane + 64 * k, U::kPieces - 1);
+        poff[k] = (uint32_t)(q / U::kCols) * row_bytes + 16u * (uint32_t)(q % U::kCols);
     }
     // unit s of the stream -> (tile slot i, unit u)
     auto load_unit = [&](uint4* buf, int s) {
         const int i = s / max(per_w, 1);
         const int u = wave + NW * (s - i * per_w);
-        const uint32_t base = s < L ? (uint32_t)(((int)blockIdx.x + G * i) * 16) * row_bytes + (uint32_t)u * kUnitRowBytes
+        const uint32_t base = s < L ? (uint32_t)(((int)blockIdx.x + G * i) * 16) * row_bytes + (uint32_t)u * U::kRowBytes
                                     : kPastEnd;
 #pragma unroll
         for (int k = 0; k < 3; ++k) buf[k] = buf_load_b128(wr, s < L ? base + poff[k] : kPastEnd);
@@ -355,7 +403,7 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
                 base[4 * (4 + k)] = d2l[3 - k];
                 base[4 * (4 + k) + 2] = d2h[3 - k];
             }
-            if (g == 0) xscale[b] = ldexpf(1.0f, e - 34);  // 2^(e-30) for X1, 1/16 for the weight bytes
+            if (g == 0) xscale[b] = ldexpf(1.0f, e - Fmt<QT>::kXScaleShift);  // 2^(e-30) for X1, / 16 or 8 for the weight bytes
         }
     }
     __syncthreads();
@@ -364,8 +412,8 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
     constexpr int kPairs = kUnitBlocks / 2;
     const int n = lane & 15;
     const int aoff = a_offset(lane);
-    const PairLane pl = pair_lane(lane);
-    const uint8_t* rowd = wbuf + n * kRowPitch;      // row n's staged blocks (scales at 18 j)
+    const PairLane pl = pair_lane<QT>(lane);
+    const uint8_t* rowd = wbuf + n * U::kPitch;      // row n's staged blocks
     float acc = 0.f;
     if constexpr (PW > 0) {
         static_assert(D % PW == 0 || PW % D == 0, "the load ring and the tile's units align");
@@ -389,14 +437,14 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
                     const int q = lane + 64 * k;
-                    if (q < kUnitPieces) park_piece(wbuf, q, buf[d][k]);
+                    if (q < U::kPieces) park_piece<QT>(wbuf, q, buf[d][k]);
                 }
                 __builtin_amdgcn_wave_barrier();
                 // the unit is parked: refill its registers before the compute,
                 // so the next unit's latency overlaps this unit's MFMAs
                 load_unit(buf[d], s + D);
                 __builtin_amdgcn_sched_barrier(0);
-                acc = chunk_dot_x<kUnitBlocks>(rowd, pl, aq[j], xsr[j], acc);
+                acc = chunk_dot_x<kUnitBlocks, QT>(rowd, pl, aq[j], xsr[j], acc);
                 __builtin_amdgcn_wave_barrier();
                 if (j == PW - 1) {  // last unit of tile s / PW
                     const float t = tile_total(acc);
@@ -414,14 +462,14 @@ __global__ __launch_bounds__(NW * 64) void q4_0_mfma_stream(const uint8_t* __res
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
                     const int q = lane + 64 * k;
-                    if (q < kUnitPieces) park_piece(wbuf, q, buf[d][k]);
+                    if (q < U::kPieces) park_piece<QT>(wbuf, q, buf[d][k]);
                 }
                 __builtin_amdgcn_wave_barrier();
                 load_unit(buf[d], s + D);
                 __builtin_amdgcn_sched_barrier(0);
                 const int i = s / per_w;
                 const int u = wave + NW * (s - i * per_w);
-                acc = chunk_dot<kUnitBlocks>(rowd, pl, xdig + u * kUnitBlocks * kXStride, aoff,
+                acc = chunk_dot<kUnitBlocks, QT>(rowd, pl, xdig + u * kUnitBlocks * kXStride, aoff,
                                              xscale + u * kUnitBlocks, acc);
                 __builtin_amdgcn_wave_barrier();
                 if (s - i * per_w == per_w - 1) {  // last unit of tile slot i
@@ -458,26 +506,26 @@ constexpr int kWideWaves = 16, kWideDepth = 1;
 constexpr int kNarrowWaves = 8, kNarrowDepth = 2;
 constexpr size_t kLdsBudget = 160 * 1024 - 256;
 
-template <int XQ, int NW, int D, int PW>
+template <int QT, int XQ, int NW, int D, int PW>
 int launch_xq(const uint8_t* w, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
-    const void* fn = (const void*)q4_0_mfma_stream<XQ, NW, D, PW>;
+    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW>;
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
-    hipLaunchKernelGGL((q4_0_mfma_stream<XQ, NW, D, PW>), dim3(grid), dim3(NW * 64), lds, st, w, x, y, M, K, o.pre,
-                       o.pre_arg, o.eps, (int)o.accumulate);
+    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW>), dim3(grid), dim3(NW * 64), lds, st, w, x, y, M, K,
+                       o.pre, o.pre_arg, o.eps, (int)o.accumulate);
     return kOk;
 }
 
 // x items (8 positions) per thread -> the matching instantiation
-template <int NW, int D>
+template <int QT, int NW, int D>
 int launch_nw(const uint8_t* w, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
     const int nb = K / 32;
     const int xq = (nb * 4 + NW * 64 - 1) / (NW * 64);
-    if (xq <= 1) return launch_xq<1, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);
-    if (xq <= 2) return launch_xq<2, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);
-    return launch_xq<4, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);  // nb <= 512, NW >= 8: at most 4 items per thread
+    if (xq <= 1) return launch_xq<QT, 1, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);
+    if (xq <= 2) return launch_xq<QT, 2, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);
+    return launch_xq<QT, 4, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);  // nb <= 512, NW >= 8: at most 4 items per thread
 }
 
 // Workgroup layout of one launch: grid size, tiles per workgroup, waves, LDS bytes.
@@ -488,21 +536,21 @@ struct StreamShape {
 
 int compute_units();
 
-size_t stream_lds(int nw, int nb, int tiles_per_group) {
-    return (size_t)nw * kSlotBytes + (size_t)nb * (kXStride + 4) + (size_t)tiles_per_group * nw * 16 * sizeof(float);
+size_t stream_lds(int slot_bytes, int nw, int nb, int tiles_per_group) {
+    return (size_t)nw * slot_bytes + (size_t)nb * (kXStride + 4) + (size_t)tiles_per_group * nw * 16 * sizeof(float);
 }
 
-StreamShape stream_shape(int64_t M, int64_t K) {
+StreamShape stream_shape(int slot_bytes, int64_t M, int64_t K) {
     const int nb = (int)(K / 32);
     const int n_tiles = (int)((M + 15) / 16);
     StreamShape sh;
     sh.grid = std::max(std::min(n_tiles, compute_units()), (n_tiles + kMaxTilesPerGroup - 1) / kMaxTilesPerGroup);
     sh.tiles_per_group = (n_tiles + sh.grid - 1) / sh.grid;
     sh.waves = kWideWaves;
-    sh.lds = stream_lds(kWideWaves, nb, sh.tiles_per_group);
+    sh.lds = stream_lds(slot_bytes, kWideWaves, nb, sh.tiles_per_group);
     if (sh.lds > kLdsBudget) {
         sh.waves = kNarrowWaves;
-        sh.lds = stream_lds(kNarrowWaves, nb, sh.tiles_per_group);
+        sh.lds = stream_lds(slot_bytes, kNarrowWaves, nb, sh.tiles_per_group);
     }
     return sh;
 }
@@ -525,33 +573,51 @@ int compute_units() {
     return cus[dev];
 }
 
-}  // namespace
-
-bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& o, int64_t M, int64_t K) {
+template <int QT>
+bool mfma_eligible(const void* w, const float* x, const MatvecOpts& o, int64_t M, int64_t K) {
     const int64_t nb = K / 32;
     return K % 256 == 0 && nb >= kUnitBlocks && nb <= kMaxBlocks && M >= 1 && M <= INT32_MAX - 16 &&
-           (M + 16) * nb * 18 < (int64_t)kPastEnd && (uintptr_t)w % 4 == 0 && (uintptr_t)x % 16 == 0 &&
+           (M + 16) * nb * Unit<QT>::kBB < (int64_t)kPastEnd && (uintptr_t)w % 4 == 0 && (uintptr_t)x % 16 == 0 &&
            (o.pre == kPreNone || (uintptr_t)o.pre_arg % 16 == 0) &&
-           stream_shape(M, K).lds <= kLdsBudget;
+           stream_shape(Unit<QT>::kSlotBytes, M, K).lds <= kLdsBudget;
 }
 
-int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st,
-                     const MatvecOpts& o) {
+template <int QT>
+int mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st, const MatvecOpts& o) {
     const int nb = (int)(K / 32);
-    const StreamShape sh = stream_shape(M, K);
+    const StreamShape sh = stream_shape(Unit<QT>::kSlotBytes, M, K);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     const int m = (int)M, k = (int)K;
     int rc;
     if (sh.waves == kWideWaves && nb / kUnitBlocks == kWideWaves)
         // K = 4096: one unit per wave and tile, the wave's x operands in registers
-        rc = launch_xq<1, kWideWaves, kWideDepth, 1>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
+        rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
     else if (sh.waves == kWideWaves)
-        rc = launch_nw<kWideWaves, kWideDepth>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
+        rc = launch_nw<QT, kWideWaves, kWideDepth>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
     else
-        rc = launch_nw<kNarrowWaves, kNarrowDepth>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
+        rc = launch_nw<QT, kNarrowWaves, kNarrowDepth>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
     if (rc) return rc;
     ASMHIP_TRY(hipGetLastError());
     return kOk;
+}
+
+}  // namespace
+
+bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& o, int64_t M, int64_t K) {
+    return mfma_eligible<kFmtQ4_0>(w, x, o, M, K);
+}
+
+int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st,
+                     const MatvecOpts& o) {
+    return mfma_launch<kFmtQ4_0>(w, x, y, M, K, st, o);
+}
+
+bool q5_0_mfma_eligible(const void* w, const float* x, int64_t M, int64_t K) {
+    return mfma_eligible<kFmtQ5_0>(w, x, MatvecOpts(), M, K);
+}
+
+int q5_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st) {
+    return mfma_launch<kFmtQ5_0>(w, x, y, M, K, st, MatvecOpts());
 }
 
 }  // namespace asmhip

@@ -531,7 +531,7 @@ def measure_traffic(timeout_s: int = 150) -> dict | None:
                     if row.get("Counter_Name") != counter:
                         continue
                     name = row["Kernel_Name"]
-                    if "q4_0_mfma" in name or "q4_matvec" in name:
+                    if "gguf_mfma_stream" in name or "q4_matvec" in name:
                         vals["matvec"].append(float(row["Counter_Value"]))
                     elif "dequant_kernel" in name:
                         vals["cal"].append(float(row["Counter_Value"]))
@@ -628,7 +628,7 @@ def main() -> None:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": round(traffic["bytes"]) if traffic else None,
             "traffic_detail": traffic,
-            "kernel": "q4_0_mfma_stream<1,16,1,1> (int8 MFMA, GGUF Q4_0)",
+            "kernel": "gguf_mfma_stream<0,1,16,1,1> (int8 MFMA, GGUF Q4_0)",
             "kernel_us_mean": round(mv["kernel_us_mean"], 3),
             "fp32_valu_kernel_us_mean": round(mv["fp32_kernel_us_mean"], 3),
             "bytes_per_launch": mv["bytes_per_step"],

@@ -5,7 +5,9 @@ threadpool dispatch threadpool.c:667-787) reads the split layout ql / qh /
 fp32 scales; the GPU also reads the same values as 22-byte GGUF Q5_0 blocks
 in place.  Bar: dequantized values bit-exact; every output row within
 1e-4 x sum_k |w[m,k]| |x[k]| of the oracle on the same bytes; the
-reference's golden inputs within TOLERANCE_Q5 (test_runner.py:35).
+reference's golden inputs within TOLERANCE_Q5 (test_runner.py:35).  GGUF
+blocks with K % 256 == 0 take the int8-MFMA stream, everything else the fp32
+VALU kernels.
 """
 
 import numpy as np
@@ -102,8 +104,9 @@ def test_q5_split_and_gguf_match_oracle(hip, oracle, M, K):
     blocks = gguf.pack_q5_0(ql, qh, d)
     y_gguf = _gguf_device(hip, blocks, x)
     assert_matvec_close(y_gguf, oracle.matmul_q5_0_gguf(blocks, x, NT), w, x)
-    # the two layouts carry the same values and take the same arithmetic
-    np.testing.assert_array_equal(y_gguf, y_split)
+    # the same values in the two layouts (GGUF blocks take the int8-MFMA stream where
+    # K % 256 == 0, the split planes the fp32 VALU kernel): within the bar of each other
+    assert_matvec_close(y_gguf, y_split, w, x)
 
 
 def test_q5_unaligned_qh_takes_the_generic_kernel(hip, oracle):
