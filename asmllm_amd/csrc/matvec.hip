@@ -659,6 +659,10 @@ int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, c
                         (long long)M, (long long)K);
         if (sel != kQ4KernelFp32 && mfma_ok) return q4_0_mfma_launch(w, x, y, M, K, stream, opts);
     }
+    if (qt == QuantType::Q4_0 && !gguf && opts.pre == kPreNone && !opts.accumulate &&
+        g_q4_kernel.load(std::memory_order_relaxed) != kQ4KernelFp32 &&
+        split_mfma_eligible(false, w, nullptr, scales, x, M, K))
+        return split_mfma_launch(false, w, nullptr, scales, x, y, M, K, stream);
     if (pairs && qt == QuantType::Q4_0) {
         const int r = pick_rows_per_wave(M, 8);
         if (gguf) {
@@ -745,6 +749,8 @@ int q5_matvec_launch(bool gguf, const void* w, const uint8_t* qh, const float* s
     const int m = (int)M, k = (int)K;
     int rc = kOk;
     if (gguf && q5_0_mfma_eligible(w, x, M, K)) return q5_0_mfma_launch(w, x, y, M, K, stream);
+    if (!gguf && split_mfma_eligible(true, w, qh, scales, x, M, K))
+        return split_mfma_launch(true, w, qh, scales, x, y, M, K, stream);
     if (pairs) {
         const int r = pick_rows_per_wave(M, 4);
         if (gguf) {

@@ -59,7 +59,7 @@ constexpr int kUnitBlocks = 8;                     // blocks per unit
 
 // GGUF block formats the stream reads in place.  A unit is 16 rows x 8 blocks;
 // each row's slice is parked in LDS at a padded pitch.
-enum BlockFmt : int { kFmtQ4_0 = 0, kFmtQ5_0 = 1 };
+enum BlockFmt : int { kFmtQ4_0 = 0, kFmtQ5_0 = 1, kFmtQ4Split = 2, kFmtQ5Split = 3 };
 template <int QT>
 struct Fmt;
 template <>
@@ -75,14 +75,32 @@ struct Fmt<kFmtQ5_0> {
     static constexpr int kRowPitch = 184;    // 46 dwords: 16 rows on 16 distinct even banks
     static constexpr int kXScaleShift = 33;  // weight bytes hold 8 (b - 16): x scale 2^(e - 30) / 8
 };
+// The reference's split layout (qs plane [M][K/32][16], Q5 qh plane [M][K/32][4],
+// fp32 scale plane [M][K/32]).  A unit row is parked as [qs 128 B | qh 32 B | scales 32 B].
+template <>
+struct Fmt<kFmtQ4Split> {
+    static constexpr int kBlockBytes = 20;   // 16 qs + 4 scale bytes per block, over two planes
+    static constexpr int kRowPitch = 168;    // 42 dwords: 16 rows on 16 distinct banks
+    static constexpr int kXScaleShift = 34;
+};
+template <>
+struct Fmt<kFmtQ5Split> {
+    static constexpr int kBlockBytes = 24;   // 16 qs + 4 qh + 4 scale bytes per block, over three planes
+    static constexpr int kRowPitch = 200;    // 50 dwords: 16 rows on 16 distinct banks
+    static constexpr int kXScaleShift = 33;
+};
 template <int QT>
 struct Unit {
+    static constexpr bool kSplit = QT == kFmtQ4Split || QT == kFmtQ5Split;
+    static constexpr bool kQ5 = QT == kFmtQ5_0 || QT == kFmtQ5Split;
     static constexpr int kBB = Fmt<QT>::kBlockBytes;
-    static constexpr int kRowBytes = kUnitBlocks * kBB;  // 144 / 176: one row's slice of a unit
-    static constexpr int kCols = kBB / 2;                // 16-byte pieces per row slice (9 / 11)
-    static constexpr int kPieces = 16 * kCols;           // 144 / 176: three 16-byte loads per lane
+    static constexpr int kRowBytes = kUnitBlocks * kBB;  // bytes of one row's slice of a unit
+    static constexpr int kCols = kBB / 2;                // 16-byte pieces per row slice
+    static constexpr int kPieces = 16 * kCols;           // 144 / 176 / 160 / 192: three 16-byte loads per lane
     static constexpr int kPitch = Fmt<QT>::kRowPitch;
     static constexpr int kSlotBytes = 16 * kPitch;       // LDS slot per wave
+    static constexpr int kQhOff = 128;                   // split layouts: row offsets of the qh and scale slices
+    static constexpr int kScOff = kQ5 ? 160 : 128;
     static_assert(kPieces <= 3 * 64, "a unit is three 16-byte loads per lane");
 };
 constexpr int kXStride = 272;                      // LDS bytes of x digits per block: [half][level*4+digit][16] + 16 pad
@@ -95,10 +113,23 @@ constexpr uint32_t kPastEnd = 0xFFFFFF00u;         // buffer offset that loads z
 // Piece q of a unit (row q / kCols, bytes 16 (q % kCols) of its slice) into
 // the wave's LDS slot at the padded row pitch (8-byte aligned: two b64 stores).
 template <int QT>
+__device__ __forceinline__ int piece_lds(int q) {
+    using U = Unit<QT>;
+    if constexpr (U::kSplit) {
+        if (q < 128) return (q >> 3) * U::kPitch + 16 * (q & 7);                  // qs
+        const int i = q - 128;
+        if (U::kQ5 && i < 32) return (i >> 1) * U::kPitch + U::kQhOff + 16 * (i & 1);  // qh
+        const int j = U::kQ5 ? i - 32 : i;
+        return (j >> 1) * U::kPitch + U::kScOff + 16 * (j & 1);                  // scales
+    } else {
+        const int r = q / U::kCols, c = q - U::kCols * r;
+        return r * U::kPitch + 16 * c;
+    }
+}
+
+template <int QT>
 __device__ __forceinline__ void park_piece(uint8_t* wbuf, int q, uint4 v) {
-    constexpr int C = Unit<QT>::kCols;
-    const int r = q / C, c = q - C * r;
-    uint2* dst = reinterpret_cast<uint2*>(wbuf + r * Unit<QT>::kPitch + 16 * c);
+    uint2* dst = reinterpret_cast<uint2*>(wbuf + piece_lds<QT>(q));
     dst[0] = make_uint2(v.x, v.y);
     dst[1] = make_uint2(v.z, v.w);
 }
@@ -158,6 +189,17 @@ template <int QT>
 __device__ __forceinline__ PairLane pair_lane(int lane) {
     constexpr int BB = Fmt<QT>::kBlockBytes;
     const int G = lane >> 4, bp = G >> 1, h = G & 1;
+    if constexpr (Unit<QT>::kSplit) {  // offsets within pair 0; pairs step 32 / 8 / 8 bytes
+        PairLane pl;
+        pl.bp = bp;
+        pl.h = h;
+        pl.qoff = 16 * bp + 8 * h;
+        pl.sh = 0u;
+        pl.hoff = Unit<QT>::kQhOff + 4 * bp;
+        pl.doff = Unit<QT>::kScOff + 4 * bp;
+        pl.dsh = 0u;
+        return pl;
+    }
     const int o = BB * bp;                  // the block's first byte within the pair
     const int qs = o + (BB - 16) + 8 * h;   // the lane's first qs byte
     PairLane pl;
@@ -187,36 +229,57 @@ __device__ __forceinline__ uint32_t q5_bytes(uint32_t nib3, uint32_t nh, int pos
 template <int NB, int QT>
 __device__ __forceinline__ float chunk_dot_x(const uint8_t* rowd, const PairLane& pl, const v4i* aq,
                                              const float* xs, float acc) {
-    constexpr int NP = NB / 2, PB = 2 * Fmt<QT>::kBlockBytes;
+    using U = Unit<QT>;
+    constexpr int NP = NB / 2;
+    // pair strides: GGUF blocks are interleaved records; split planes step 32 (qs), 8 (qh, scales)
+    constexpr int PQ = U::kSplit ? 32 : 2 * Fmt<QT>::kBlockBytes;
+    constexpr int PH = U::kSplit ? 8 : PQ;
     v4i bq[NP];
     uint32_t sc[NP];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-        const uint8_t* pr = rowd + PB * p;
-        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(pr + pl.qoff);
-        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(pr + pl.qoff + 4);
-        const uint32_t w2 = *reinterpret_cast<const uint32_t*>(pr + pl.qoff + 8);
-        const uint32_t qa = __builtin_amdgcn_alignbyte(w1, w0, pl.sh);  // qs bytes 8h..8h+3
-        const uint32_t qb = __builtin_amdgcn_alignbyte(w2, w1, pl.sh);  // qs bytes 8h+4..8h+7
-        if constexpr (QT == kFmtQ4_0) {
+        const uint8_t* pq = rowd + PQ * p + pl.qoff;
+        uint32_t qa, qb;  // qs bytes 8h..8h+3 and 8h+4..8h+7 of the lane's block
+        if constexpr (U::kSplit) {
+            qa = *reinterpret_cast<const uint32_t*>(pq);
+            qb = *reinterpret_cast<const uint32_t*>(pq + 4);
+        } else {
+            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(pq);
+            const uint32_t w1 = *reinterpret_cast<const uint32_t*>(pq + 4);
+            const uint32_t w2 = *reinterpret_cast<const uint32_t*>(pq + 8);
+            qa = __builtin_amdgcn_alignbyte(w1, w0, pl.sh);
+            qb = __builtin_amdgcn_alignbyte(w2, w1, pl.sh);
+        }
+        if constexpr (!U::kQ5) {
             const long la = pack_q4(qa), lb = pack_q4(qb);  // (lo | hi << 32) of each dword
             bq[p] = (v4i){(int)(uint32_t)la, (int)(uint32_t)lb, (int)(uint32_t)(la >> 32), (int)(uint32_t)(lb >> 32)};
         } else {
-            const uint32_t h0 = *reinterpret_cast<const uint32_t*>(pr + pl.hoff);
-            const uint32_t h1 = *reinterpret_cast<const uint32_t*>(pr + pl.hoff + 4);
-            const uint32_t nh = ~__builtin_amdgcn_alignbyte(h1, h0, pl.sh);
+            const uint8_t* ph = rowd + PH * p + pl.hoff;
+            uint32_t hq;
+            if constexpr (U::kSplit) {
+                hq = *reinterpret_cast<const uint32_t*>(ph);
+            } else {
+                const uint32_t h0 = *reinterpret_cast<const uint32_t*>(ph);
+                const uint32_t h1 = *reinterpret_cast<const uint32_t*>(ph + 4);
+                hq = __builtin_amdgcn_alignbyte(h1, h0, pl.sh);
+            }
+            const uint32_t nh = ~hq;
             const int b0 = 8 * pl.h;
             bq[p] = (v4i){(int)q5_bytes(qa << 3, nh, b0), (int)q5_bytes(qb << 3, nh, b0 + 4),
                           (int)q5_bytes(qa >> 1, nh, 16 + b0), (int)q5_bytes(qb >> 1, nh, 20 + b0)};
         }
-        sc[p] = *reinterpret_cast<const uint32_t*>(pr + pl.doff) >> pl.dsh;
+        sc[p] = *reinterpret_cast<const uint32_t*>(rowd + PH * p + pl.doff) >> pl.dsh;
     }
     const v4i z = {0, 0, 0, 0};
     v4i d[NP];
 #pragma unroll
     for (int p = 0; p < NP; ++p) d[p] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aq[p], bq[p], z, 0, 0, 0);
 #pragma unroll
-    for (int p = 0; p < NP; ++p) acc = fmaf(block_value(d[p]) * xs[p], half_lo(sc[p]), acc);
+    for (int p = 0; p < NP; ++p) {
+        // GGUF: fp16 scale (converted inside the FMA); split: the fp32 scale itself
+        const float dw = U::kSplit ? __uint_as_float(sc[p]) : half_lo(sc[p]);
+        acc = fmaf(block_value(d[p]) * xs[p], dw, acc);
+    }
     return acc;
 }
 
@@ -255,6 +318,8 @@ __device__ __forceinline__ float tile_total(float acc) {
 // any K, operands read from LDS per unit.
 template <int QT, int XQ, int NW, int D, int PW>
 __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __restrict__ w,
+                                                            const uint8_t* __restrict__ wh,
+                                                            const float* __restrict__ wsc,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int M, int K, int pre, const float* __restrict__ pre_arg,
                                                             float eps, int accumulate) {
@@ -264,7 +329,9 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     __shared__ float red[NW];
     const int nb = K >> 5;
     const int nu = nb / kUnitBlocks;  // units per tile
-    const uint32_t row_bytes = (uint32_t)nb * (uint32_t)U::kBB;
+    // GGUF: one record plane of kBB bytes per block; split: qs 16, qh 4, scales 4 bytes per block
+    const uint32_t row_bytes = (uint32_t)nb * (uint32_t)(U::kSplit ? 16 : U::kBB);
+    const uint32_t row_bytes4 = (uint32_t)nb * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int G = gridDim.x;
     const int n_tiles = (M + 15) >> 4;
@@ -272,6 +339,8 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     const int per_w = wave < nu ? (nu - wave + NW - 1) / NW : 0;  // this wave's units per tile
     const int L = my_tiles * per_w;                              // length of this wave's stream
     const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
+    const auto hr = make_rsrc(U::kQ5 && U::kSplit ? wh : w, U::kQ5 && U::kSplit ? row_bytes4 * (uint32_t)M : 0u);
+    const auto sr = make_rsrc(U::kSplit ? (const void*)wsc : (const void*)w, U::kSplit ? row_bytes4 * (uint32_t)M : 0u);
     uint8_t* wbuf = lds + wave * U::kSlotBytes;
     uint8_t* xdig = lds + NW * U::kSlotBytes;
     float* xscale = reinterpret_cast<float*>(xdig + nb * kXStride);
@@ -280,20 +349,43 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     // This lane's three 16-byte pieces of a unit: piece q = row q / kCols,
     // bytes 16 (q % kCols) of the row's slice.  Rows past M fall beyond the
     // buffer and load zeros.
+    // Split layouts: loads 0-1 are qs pieces (row q / 8, bytes 16 (q % 8) of the row's 128-byte
+    // qs slice); load 2 of lanes 0-31 (Q5: lanes 32-63 too) reads 16 bytes of a row's 32-byte qh
+    // or scale slice (row i / 2, half i % 2).
     uint32_t poff[3];
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         const int q = min(lane + 64 * k, U::kPieces - 1);
-        poff[k] = (uint32_t)(q / U::kCols) * row_bytes + 16u * (uint32_t)(q % U::kCols);
+        if constexpr (U::kSplit) {
+            const int i = (q >= 128 ? q - 128 : q) & 31;
+            poff[k] = q < 128 ? (uint32_t)(q >> 3) * row_bytes + 16u * (uint32_t)(q & 7)
+                              : (uint32_t)(i >> 1) * row_bytes4 + 16u * (uint32_t)(i & 1);
+        } else {
+            poff[k] = (uint32_t)(q / U::kCols) * row_bytes + 16u * (uint32_t)(q % U::kCols);
+        }
     }
     // unit s of the stream -> (tile slot i, unit u)
     auto load_unit = [&](uint4* buf, int s) {
         const int i = s / max(per_w, 1);
         const int u = wave + NW * (s - i * per_w);
-        const uint32_t base = s < L ? (uint32_t)(((int)blockIdx.x + G * i) * 16) * row_bytes + (uint32_t)u * U::kRowBytes
+        const uint32_t row0 = (uint32_t)(((int)blockIdx.x + G * i) * 16);
+        const uint32_t base = s < L ? row0 * row_bytes + (uint32_t)u * (U::kSplit ? 128u : (uint32_t)U::kRowBytes)
                                     : kPastEnd;
+        if constexpr (U::kSplit) {
+            const uint32_t base4 = s < L ? row0 * row_bytes4 + (uint32_t)u * 32u : kPastEnd;
+            buf[0] = buf_load_b128(wr, s < L ? base + poff[0] : kPastEnd);
+            buf[1] = buf_load_b128(wr, s < L ? base + poff[1] : kPastEnd);
+            const uint32_t o2 = s < L ? base4 + poff[2] : kPastEnd;
+            if (U::kQ5 ? lane < 32 : false)
+                buf[2] = buf_load_b128(hr, o2);
+            else if (U::kQ5 || lane < 32)
+                buf[2] = buf_load_b128(sr, o2);
+            else
+                buf[2] = make_uint4(0, 0, 0, 0);
+        } else {
 #pragma unroll
-        for (int k = 0; k < 3; ++k) buf[k] = buf_load_b128(wr, s < L ? base + poff[k] : kPastEnd);
+            for (int k = 0; k < 3; ++k) buf[k] = buf_load_b128(wr, s < L ? base + poff[k] : kPastEnd);
+        }
     };
 
     // 1) x (and the pre-op argument) first.  Item it = (block it / 4, k-group
@@ -506,26 +598,33 @@ constexpr int kWideWaves = 16, kWideDepth = 1;
 constexpr int kNarrowWaves = 8, kNarrowDepth = 2;
 constexpr size_t kLdsBudget = 160 * 1024 - 256;
 
+// The weight planes of one launch: GGUF blocks in w, or the split qs / qh / scale planes.
+struct Planes {
+    const uint8_t* w;
+    const uint8_t* wh;
+    const float* wsc;
+};
+
 template <int QT, int XQ, int NW, int D, int PW>
-int launch_xq(const uint8_t* w, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
+int launch_xq(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
     const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW>;
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
-    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW>), dim3(grid), dim3(NW * 64), lds, st, w, x, y, M, K,
-                       o.pre, o.pre_arg, o.eps, (int)o.accumulate);
+    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW>), dim3(grid), dim3(NW * 64), lds, st, pw.w, pw.wh,
+                       pw.wsc, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate);
     return kOk;
 }
 
 // x items (8 positions) per thread -> the matching instantiation
 template <int QT, int NW, int D>
-int launch_nw(const uint8_t* w, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
+int launch_nw(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
     const int nb = K / 32;
     const int xq = (nb * 4 + NW * 64 - 1) / (NW * 64);
-    if (xq <= 1) return launch_xq<QT, 1, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);
-    if (xq <= 2) return launch_xq<QT, 2, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);
-    return launch_xq<QT, 4, NW, D, 0>(w, x, y, M, K, grid, lds, st, o);  // nb <= 512, NW >= 8: at most 4 items per thread
+    if (xq <= 1) return launch_xq<QT, 1, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);
+    if (xq <= 2) return launch_xq<QT, 2, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);
+    return launch_xq<QT, 4, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);  // nb <= 512, NW >= 8: at most 4 items per thread
 }
 
 // Workgroup layout of one launch: grid size, tiles per workgroup, waves, LDS bytes.
@@ -574,28 +673,32 @@ int compute_units() {
 }
 
 template <int QT>
-bool mfma_eligible(const void* w, const float* x, const MatvecOpts& o, int64_t M, int64_t K) {
+bool mfma_eligible(const Planes& pw, const float* x, const MatvecOpts& o, int64_t M, int64_t K) {
+    using U = Unit<QT>;
     const int64_t nb = K / 32;
+    const int64_t plane = (M + 16) * nb * (U::kSplit ? 16 : U::kBB);  // largest plane, with the last tile's padding
+    bool aligned = (uintptr_t)pw.w % 4 == 0;
+    if (U::kSplit) aligned = (uintptr_t)pw.w % 16 == 0 && (uintptr_t)pw.wsc % 16 == 0 && (!U::kQ5 || (uintptr_t)pw.wh % 16 == 0);
     return K % 256 == 0 && nb >= kUnitBlocks && nb <= kMaxBlocks && M >= 1 && M <= INT32_MAX - 16 &&
-           (M + 16) * nb * Unit<QT>::kBB < (int64_t)kPastEnd && (uintptr_t)w % 4 == 0 && (uintptr_t)x % 16 == 0 &&
+           plane < (int64_t)kPastEnd && aligned && (uintptr_t)x % 16 == 0 &&
            (o.pre == kPreNone || (uintptr_t)o.pre_arg % 16 == 0) &&
-           stream_shape(Unit<QT>::kSlotBytes, M, K).lds <= kLdsBudget;
+           stream_shape(U::kSlotBytes, M, K).lds <= kLdsBudget;
 }
 
 template <int QT>
-int mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st, const MatvecOpts& o) {
+int mfma_launch(const Planes& pw, const float* x, float* y, int64_t M, int64_t K, hipStream_t st,
+                const MatvecOpts& o) {
     const int nb = (int)(K / 32);
     const StreamShape sh = stream_shape(Unit<QT>::kSlotBytes, M, K);
-    const uint8_t* wb = static_cast<const uint8_t*>(w);
     const int m = (int)M, k = (int)K;
     int rc;
     if (sh.waves == kWideWaves && nb / kUnitBlocks == kWideWaves)
         // K = 4096: one unit per wave and tile, the wave's x operands in registers
-        rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
+        rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
     else if (sh.waves == kWideWaves)
-        rc = launch_nw<QT, kWideWaves, kWideDepth>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
+        rc = launch_nw<QT, kWideWaves, kWideDepth>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
     else
-        rc = launch_nw<QT, kNarrowWaves, kNarrowDepth>(wb, x, y, m, k, sh.grid, sh.lds, st, o);
+        rc = launch_nw<QT, kNarrowWaves, kNarrowDepth>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
     if (rc) return rc;
     ASMHIP_TRY(hipGetLastError());
     return kOk;
@@ -604,20 +707,35 @@ int mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, h
 }  // namespace
 
 bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& o, int64_t M, int64_t K) {
-    return mfma_eligible<kFmtQ4_0>(w, x, o, M, K);
+    return mfma_eligible<kFmtQ4_0>(Planes{static_cast<const uint8_t*>(w), nullptr, nullptr}, x, o, M, K);
 }
 
 int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st,
                      const MatvecOpts& o) {
-    return mfma_launch<kFmtQ4_0>(w, x, y, M, K, st, o);
+    return mfma_launch<kFmtQ4_0>(Planes{static_cast<const uint8_t*>(w), nullptr, nullptr}, x, y, M, K, st, o);
 }
 
 bool q5_0_mfma_eligible(const void* w, const float* x, int64_t M, int64_t K) {
-    return mfma_eligible<kFmtQ5_0>(w, x, MatvecOpts(), M, K);
+    return mfma_eligible<kFmtQ5_0>(Planes{static_cast<const uint8_t*>(w), nullptr, nullptr}, x, MatvecOpts(), M, K);
 }
 
 int q5_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st) {
-    return mfma_launch<kFmtQ5_0>(w, x, y, M, K, st, MatvecOpts());
+    return mfma_launch<kFmtQ5_0>(Planes{static_cast<const uint8_t*>(w), nullptr, nullptr}, x, y, M, K, st,
+                                 MatvecOpts());
+}
+
+bool split_mfma_eligible(bool q5, const void* qs, const uint8_t* qh, const float* scales, const float* x, int64_t M,
+                         int64_t K) {
+    const Planes pw{static_cast<const uint8_t*>(qs), qh, scales};
+    return q5 ? mfma_eligible<kFmtQ5Split>(pw, x, MatvecOpts(), M, K)
+              : mfma_eligible<kFmtQ4Split>(pw, x, MatvecOpts(), M, K);
+}
+
+int split_mfma_launch(bool q5, const void* qs, const uint8_t* qh, const float* scales, const float* x, float* y,
+                      int64_t M, int64_t K, hipStream_t st) {
+    const Planes pw{static_cast<const uint8_t*>(qs), qh, scales};
+    return q5 ? mfma_launch<kFmtQ5Split>(pw, x, y, M, K, st, MatvecOpts())
+              : mfma_launch<kFmtQ4Split>(pw, x, y, M, K, st, MatvecOpts());
 }
 
 }  // namespace asmhip

@@ -252,15 +252,16 @@ MATVEC_TABLE = [
     ("llama3 gate 14336x4096", "q4", 14336, 4096),
     ("llama3 up 14336x4096", "q4", 14336, 4096),
     ("llama3 down 4096x14336", "q4", 4096, 14336),
+    ("q4 split 11008x4096", "q4s", 11008, 4096),
     ("q5_0 11008x4096", "q5", 11008, 4096),
     ("q5 split 11008x4096", "q5s", 11008, 4096),
 ]
 
 
-def _rotating_q5(M: int, K: int, copies: int, seed: int, split: bool):
+def _rotating_q5(M: int, K: int, copies: int, seed: int, split: bool, q4: bool = False):
     """`copies` device copies of one synthetic Q5_0 matrix (random nibbles and
     fifth bits, fp16 scales of N(0, 0.02^2) weights' size): GGUF blocks, or
-    the split ql / qh / fp32 scales planes."""
+    the split ql / qh / fp32 scales planes (q4: the Q4 split qs / scales planes)."""
     from asmllm_amd import gguf
     from asmllm_amd.device import DeviceBuffer
 
@@ -269,7 +270,10 @@ def _rotating_q5(M: int, K: int, copies: int, seed: int, split: bool):
     ql = rng.integers(0, 256, (M, nb, 16), dtype=np.uint8)
     qh = rng.integers(0, 256, (M, nb, 4), dtype=np.uint8)
     d = (rng.uniform(0.001, 0.004, (M, nb)) * rng.choice([-1.0, 1.0], (M, nb))).astype(np.float16)
-    planes = (ql, qh, d.astype(np.float32)) if split else (gguf.pack_q5_0(ql, qh, d),)
+    if q4:
+        planes = (ql, d.astype(np.float32))
+    else:
+        planes = (ql, qh, d.astype(np.float32)) if split else (gguf.pack_q5_0(ql, qh, d),)
     first = [DeviceBuffer.from_numpy(a) for a in planes]
     sets = [first]
     for _ in range(copies - 1):
@@ -291,13 +295,17 @@ def bench_matvec_table(min_rotated_bytes: int = 600_000_000) -> list[dict]:
     lib = native.lib()
     rows = []
     for name, qt, M, K in MATVEC_TABLE:
-        blk = {"q4": 18, "q8": 34, "q5": 22, "q5s": 24}[qt]
+        blk = {"q4": 18, "q8": 34, "q5": 22, "q5s": 24, "q4s": 20}[qt]
         copies = max(8, -(-min_rotated_bytes // (M * (K // 32) * blk)))
         dx, dy = DeviceBuffer(4 * K), DeviceBuffer(4 * M)
         native.check(lib.asmhip_fill_f32(dx.ptr, K, 0.5, None), "fill")
-        if qt in ("q5", "q5s"):
-            sets, _ = _rotating_q5(M, K, copies, seed=M * 7 + K, split=qt == "q5s")
-            if qt == "q5":
+        if qt in ("q5", "q5s", "q4s"):
+            sets, _ = _rotating_q5(M, K, copies, seed=M * 7 + K, split=qt != "q5", q4=qt == "q4s")
+            if qt == "q4s":
+                def enqueue(i, st, sets=sets, dx=dx, dy=dy, M=M, K=K, name=name):
+                    qs, sc = sets[i % len(sets)]
+                    native.check(lib.asmhip_matmul_q4_split(qs.ptr, sc.ptr, dx.ptr, dy.ptr, M, K, st), name)
+            elif qt == "q5":
                 def enqueue(i, st, sets=sets, dx=dx, dy=dy, M=M, K=K, name=name):
                     w = sets[i % len(sets)]
                     native.check(lib.asmhip_matmul_q5_0(w[0].ptr, dx.ptr, dy.ptr, M, K, st), name)

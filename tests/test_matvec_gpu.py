@@ -247,6 +247,25 @@ def test_split_layout_device_pointers(hip, oracle):
     np.testing.assert_array_equal(dy.download(np.float32, 2048), y)
 
 
+@pytest.mark.parametrize("M,K", [(1, 256), (300, 2304), (2048, 4096), (11008, 4096), (4096, 11008), (64, 16384),
+                                 (33, 2080)])
+def test_split_layout_both_kernels(hip, oracle, q4_kernel, M, K):
+    """The reference's split layout through asmhip_matmul_q4_split: the int8-MFMA
+    stream (K % 256 == 0, planes 16-byte aligned) and the fp32 VALU kernel
+    (forced, and for K = 2080) both within the bar of the oracle's AVX2 kernel."""
+    blocks, x = _weights(M + K, M, K)
+    qs, sc = gguf.split_q4_0(blocks)
+    ref = oracle.matmul_q4_mt(qs, sc, x, NT)
+    w = oracle.dequantize_q4_0(blocks)
+    dq, ds, dx, dy = (DeviceBuffer.from_numpy(qs), DeviceBuffer.from_numpy(sc), DeviceBuffer.from_numpy(x),
+                      DeviceBuffer(M * 4))
+    for kernel in (native.Q4_KERNEL_AUTO, native.Q4_KERNEL_FP32):
+        q4_kernel(kernel)
+        assert hip.asmhip_matmul_q4_split(dq.ptr, ds.ptr, dx.ptr, dy.ptr, M, K, None) == 0, hip.asmhip_last_error()
+        synchronize()
+        assert_matvec_close(dy.download(np.float32, M), ref, w, x)
+
+
 def test_bad_arguments_are_rejected(hip):
     dx, dy, db = DeviceBuffer(4096 * 4), DeviceBuffer(64 * 4), DeviceBuffer(64 * 128 * 18)
     assert hip.asmhip_matmul_q4_0(db.ptr, dx.ptr, dy.ptr, 64, 4010, None) == -1
