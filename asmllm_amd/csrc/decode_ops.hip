@@ -198,6 +198,21 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(const float* __restri
 // rounded to fp16 and written to the caches at `pos` (by the workgroup of the
 // first query head of the kv group), and the workgroup whose split holds `pos`
 // uses those fp16 values instead of reading the row it writes.
+// Sum over aligned groups of N lanes (N = 8 or 16), every lane receiving its
+// group's sum, with DPP adds instead of LDS permutes: quad_perm [1,0,3,2] and
+// [2,3,0,1] sum the quads, row_half_mirror pairs quad 0 with 1 (2 with 3),
+// row_mirror the two halves of a 16-lane row.  Each step adds two partial sums
+// that are the same in every lane of a pair, so all lanes hold the same bits.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 8 || N == 16, "8- or 16-lane groups");
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+    if constexpr (N == 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+    return v;
+}
+
 // E fp16 values of one cache row slice (E = 8: one 16-byte access; E = 6: three dwords).
 template <int E>
 struct HalfRow {
@@ -254,12 +269,18 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     const size_t head_off = (size_t)kvh * max_ctx * HD + E * c;
 
     // all k and v rows of this lane, issued up front
+    // all k rows first, then all v rows: the scores can start while v is in flight
     HalfRow<E> kr[kRows], vr[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         const int p = p0 + r * kRowPos + w * kGroups + g;
         const bool live = p < p1 && !(ROPE && p == pos);
         kr[r] = live ? HalfRow<E>::load(kc + head_off + (size_t)p * HD) : HalfRow<E>::zero();
+    }
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const int p = p0 + r * kRowPos + w * kGroups + g;
+        const bool live = p < p1 && !(ROPE && p == pos);
         vr[r] = live ? HalfRow<E>::load(vc + head_off + (size_t)p * HD) : HalfRow<E>::zero();
     }
     float qv[E];
@@ -317,8 +338,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
             d = fmaf(qv[2 * t], half_lo(kr[r].w[t]), d);
             d = fmaf(qv[2 * t + 1], half_hi(kr[r].w[t]), d);
         }
-#pragma unroll
-        for (int o = kLanes / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, kWave);
+        d = group_sum<kLanes>(d);
         const int p = p0 + r * kRowPos + w * kGroups + g;
         sc[r] = p < p1 ? d : -INFINITY;
         m = fmaxf(m, sc[r]);
@@ -329,7 +349,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     if (m != -INFINITY) {
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
-            const float e = expf(sc[r] - m);  // 0 for positions past the split
+            const float e = __expf(sc[r] - m);  // 0 for positions past the split
             l += e;
 #pragma unroll
             for (int t = 0; t < E / 2; ++t) {
@@ -343,7 +363,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     for (int o = kLanes; o < kWave; o <<= 1) {
         const float m2 = __shfl_xor(m, o, kWave), l2 = __shfl_xor(l, o, kWave);
         const float M = fmaxf(m, m2);
-        const float f1 = M == -INFINITY ? 0.f : expf(m - M), f2 = M == -INFINITY ? 0.f : expf(m2 - M);
+        const float f1 = M == -INFINITY ? 0.f : __expf(m - M), f2 = M == -INFINITY ? 0.f : __expf(m2 - M);
         l = l * f1 + l2 * f2;
 #pragma unroll
         for (int t = 0; t < E; ++t) acc[t] = acc[t] * f1 + __shfl_xor(acc[t], o, kWave) * f2;
@@ -365,7 +385,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
         if (M != -INFINITY) {
 #pragma unroll
             for (int i = 0; i < kBlock / kWave; ++i) {
-                const float f = expf(wst[i][0] - M);
+                const float f = __expf(wst[i][0] - M);
                 L = fmaf(wst[i][1], f, L);
                 a = fmaf(wst[i][2 + threadIdx.x], f, a);
             }
@@ -394,7 +414,7 @@ __global__ __launch_bounds__(HD) void attn_decode_merge(const float* __restrict_
     if (M != -INFINITY) {
 #pragma unroll 8
         for (int i = 0; i < S; ++i) {
-            const float f = expf(sm[i] - M);
+            const float f = __expf(sm[i] - M);
             L = fmaf(sl[i], f, L);
             a = fmaf(ph[(size_t)i * (HD + 2) + 2 + threadIdx.x], f, a);
         }
