@@ -51,11 +51,16 @@ int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t
 // The same stream over 22-byte GGUF Q5_0 blocks (no fused pre-ops).
 bool q5_0_mfma_eligible(const void* w, const float* x, int64_t M, int64_t K);
 int q5_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t stream);
-// The same stream over the reference's split layout: Q4 (qs + fp32 scales) or
-// Q5 (ql + qh + fp32 scales) planes; K % 256 == 0, 16-byte aligned planes.
-bool split_mfma_eligible(bool q5, const void* qs, const uint8_t* qh, const float* scales, const float* x, int64_t M,
+// The same stream over 34-byte GGUF Q8_0 blocks.
+bool q8_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& opts, int64_t M, int64_t K);
+int q8_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t stream,
+                     const MatvecOpts& opts);
+// The same stream over the reference's split layout, bits = 4 (qs + fp32 scales),
+// 5 (ql + qh + fp32 scales) or 8 (int8 qs + fp32 scales); K % 256 == 0, 16-byte
+// aligned planes.
+bool split_mfma_eligible(int bits, const void* qs, const uint8_t* qh, const float* scales, const float* x, int64_t M,
                          int64_t K);
-int split_mfma_launch(bool q5, const void* qs, const uint8_t* qh, const float* scales, const float* x, float* y,
+int split_mfma_launch(int bits, const void* qs, const uint8_t* qh, const float* scales, const float* x, float* y,
                       int64_t M, int64_t K, hipStream_t stream);
 
 // C[T][M] = A (Q8_0 blocks [T][K/32]) x W (Q8_0 blocks [M][K/32])^T, block dots

@@ -661,8 +661,13 @@ int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, c
     }
     if (qt == QuantType::Q4_0 && !gguf && opts.pre == kPreNone && !opts.accumulate &&
         g_q4_kernel.load(std::memory_order_relaxed) != kQ4KernelFp32 &&
-        split_mfma_eligible(false, w, nullptr, scales, x, M, K))
-        return split_mfma_launch(false, w, nullptr, scales, x, y, M, K, stream);
+        split_mfma_eligible(4, w, nullptr, scales, x, M, K))
+        return split_mfma_launch(4, w, nullptr, scales, x, y, M, K, stream);
+    if (qt == QuantType::Q8_0 && g_q4_kernel.load(std::memory_order_relaxed) != kQ4KernelFp32) {
+        if (gguf && q8_0_mfma_eligible(w, x, opts, M, K)) return q8_0_mfma_launch(w, x, y, M, K, stream, opts);
+        if (!gguf && opts.pre == kPreNone && !opts.accumulate && split_mfma_eligible(8, w, nullptr, scales, x, M, K))
+            return split_mfma_launch(8, w, nullptr, scales, x, y, M, K, stream);
+    }
     if (pairs && qt == QuantType::Q4_0) {
         const int r = pick_rows_per_wave(M, 8);
         if (gguf) {
@@ -748,9 +753,10 @@ int q5_matvec_launch(bool gguf, const void* w, const uint8_t* qh, const float* s
     const bool pairs = nb % 2 == 0 && aligned && lds <= 160 * 1024 - 256 && total < (int64_t)UINT32_MAX;
     const int m = (int)M, k = (int)K;
     int rc = kOk;
-    if (gguf && q5_0_mfma_eligible(w, x, M, K)) return q5_0_mfma_launch(w, x, y, M, K, stream);
-    if (!gguf && split_mfma_eligible(true, w, qh, scales, x, M, K))
-        return split_mfma_launch(true, w, qh, scales, x, y, M, K, stream);
+    const bool mfma = g_q4_kernel.load(std::memory_order_relaxed) != kQ4KernelFp32;
+    if (mfma && gguf && q5_0_mfma_eligible(w, x, M, K)) return q5_0_mfma_launch(w, x, y, M, K, stream);
+    if (mfma && !gguf && split_mfma_eligible(5, w, qh, scales, x, M, K))
+        return split_mfma_launch(5, w, qh, scales, x, y, M, K, stream);
     if (pairs) {
         const int r = pick_rows_per_wave(M, 4);
         if (gguf) {

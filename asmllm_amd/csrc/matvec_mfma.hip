@@ -57,51 +57,79 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kUnitBlocks = 8;                     // blocks per unit
 
-// GGUF block formats the stream reads in place.  A unit is 16 rows x 8 blocks;
-// each row's slice is parked in LDS at a padded pitch.
-enum BlockFmt : int { kFmtQ4_0 = 0, kFmtQ5_0 = 1, kFmtQ4Split = 2, kFmtQ5Split = 3 };
+// Block formats the stream reads in place.  A unit is 16 rows x 8 blocks; each
+// row's slice is parked in LDS at a padded pitch (pitches chosen so that the
+// operand reads of the 16 rows fall on 16 distinct banks).
+enum BlockFmt : int {
+    kFmtQ4_0 = 0, kFmtQ5_0 = 1, kFmtQ4Split = 2, kFmtQ5Split = 3, kFmtQ8_0 = 4, kFmtQ8Split = 5
+};
 template <int QT>
 struct Fmt;
 template <>
 struct Fmt<kFmtQ4_0> {
     static constexpr int kBlockBytes = 18;   // fp16 d, qs[16]
-    static constexpr int kRowPitch = 152;    // 38 dwords: the operand reads of 16 rows hit distinct
-                                             // banks (a 144-byte pitch pairs rows n and n + 8)
+    static constexpr int kQsBytes = 16;
+    static constexpr int kRowPitch = 152;    // 38 dwords (a 144-byte pitch pairs rows n and n + 8)
     static constexpr int kXScaleShift = 34;  // weight bytes hold 16 (n - 8): x scale 2^(e - 30) / 16
 };
 template <>
 struct Fmt<kFmtQ5_0> {
     static constexpr int kBlockBytes = 22;   // fp16 d, qh[4], qs[16]
-    static constexpr int kRowPitch = 184;    // 46 dwords: 16 rows on 16 distinct even banks
+    static constexpr int kQsBytes = 16;
+    static constexpr int kRowPitch = 184;    // 46 dwords
     static constexpr int kXScaleShift = 33;  // weight bytes hold 8 (b - 16): x scale 2^(e - 30) / 8
 };
-// The reference's split layout (qs plane [M][K/32][16], Q5 qh plane [M][K/32][4],
-// fp32 scale plane [M][K/32]).  A unit row is parked as [qs 128 B | qh 32 B | scales 32 B].
+template <>
+struct Fmt<kFmtQ8_0> {
+    static constexpr int kBlockBytes = 34;   // fp16 d, qs[32] (int8)
+    static constexpr int kQsBytes = 32;
+    static constexpr int kRowPitch = 280;    // 70 dwords
+    static constexpr int kXScaleShift = 30;  // weight bytes are the int8 values themselves
+};
+// The reference's split layout: a qs plane [M][K/32][16 or 32], for Q5 a qh plane
+// [M][K/32][4], and an fp32 scale plane [M][K/32].  A unit row is parked as
+// [qs slice | qh 32 B | scales 32 B].
 template <>
 struct Fmt<kFmtQ4Split> {
-    static constexpr int kBlockBytes = 20;   // 16 qs + 4 scale bytes per block, over two planes
-    static constexpr int kRowPitch = 168;    // 42 dwords: 16 rows on 16 distinct banks
+    static constexpr int kBlockBytes = 20;   // per block over the planes: 16 qs + 4 scale bytes
+    static constexpr int kQsBytes = 16;
+    static constexpr int kRowPitch = 168;    // 42 dwords
     static constexpr int kXScaleShift = 34;
 };
 template <>
 struct Fmt<kFmtQ5Split> {
-    static constexpr int kBlockBytes = 24;   // 16 qs + 4 qh + 4 scale bytes per block, over three planes
-    static constexpr int kRowPitch = 200;    // 50 dwords: 16 rows on 16 distinct banks
+    static constexpr int kBlockBytes = 24;   // 16 qs + 4 qh + 4 scale bytes
+    static constexpr int kQsBytes = 16;
+    static constexpr int kRowPitch = 200;    // 50 dwords
     static constexpr int kXScaleShift = 33;
+};
+template <>
+struct Fmt<kFmtQ8Split> {
+    static constexpr int kBlockBytes = 36;   // 32 qs + 4 scale bytes
+    static constexpr int kQsBytes = 32;
+    static constexpr int kRowPitch = 296;    // 74 dwords
+    static constexpr int kXScaleShift = 30;
 };
 template <int QT>
 struct Unit {
-    static constexpr bool kSplit = QT == kFmtQ4Split || QT == kFmtQ5Split;
+    static constexpr bool kSplit = QT == kFmtQ4Split || QT == kFmtQ5Split || QT == kFmtQ8Split;
     static constexpr bool kQ5 = QT == kFmtQ5_0 || QT == kFmtQ5Split;
+    static constexpr bool kQ8 = QT == kFmtQ8_0 || QT == kFmtQ8Split;
     static constexpr int kBB = Fmt<QT>::kBlockBytes;
-    static constexpr int kRowBytes = kUnitBlocks * kBB;  // bytes of one row's slice of a unit
-    static constexpr int kCols = kBB / 2;                // 16-byte pieces per row slice
-    static constexpr int kPieces = 16 * kCols;           // 144 / 176 / 160 / 192: three 16-byte loads per lane
+    static constexpr int kQsPerBlock = Fmt<QT>::kQsBytes;
+    // main plane (GGUF records, or the split qs plane): bytes per block, per row slice, pieces
+    static constexpr int kMainPerBlock = kSplit ? kQsPerBlock : kBB;
+    static constexpr int kMainRow = kUnitBlocks * kMainPerBlock;  // 144 / 176 / 272 / 128 / 128 / 256
+    static constexpr int kCols = kMainRow / 16;                    // 16-byte pieces per row slice
+    static constexpr int kMainPieces = 16 * kCols;
+    static constexpr int kQhOff = kMainRow;                        // split: row offsets of the qh / scale slices
+    static constexpr int kScOff = kMainRow + (kQ5 && kSplit ? 32 : 0);
+    static constexpr int kPieces = kMainPieces + (kSplit ? (kQ5 ? 64 : 32) : 0);
+    static constexpr int kLoads = (kPieces + 63) / 64;             // 16-byte loads per lane: 3 (Q4, Q5) or 5 (Q8)
     static constexpr int kPitch = Fmt<QT>::kRowPitch;
-    static constexpr int kSlotBytes = 16 * kPitch;       // LDS slot per wave
-    static constexpr int kQhOff = 128;                   // split layouts: row offsets of the qh and scale slices
-    static constexpr int kScOff = kQ5 ? 160 : 128;
-    static_assert(kPieces <= 3 * 64, "a unit is three 16-byte loads per lane");
+    static constexpr int kSlotBytes = 16 * kPitch;                 // LDS slot per wave
+    static_assert(kMainRow % 16 == 0 && (!kSplit || kMainPieces % 64 == 0), "piece layout");
+    static_assert(kPitch >= kScOff + (kSplit ? 32 : 0) && kPitch % 8 == 0, "row pitch");
 };
 constexpr int kXStride = 272;                      // LDS bytes of x digits per block: [half][level*4+digit][16] + 16 pad
                                                    // (16-byte rows for the 16-byte A operands)
@@ -110,21 +138,21 @@ constexpr int kMaxBlocks = 512;                    // K <= 16384
 constexpr int kMaxTilesPerGroup = 8;
 constexpr uint32_t kPastEnd = 0xFFFFFF00u;         // buffer offset that loads zeros
 
-// Piece q of a unit (row q / kCols, bytes 16 (q % kCols) of its slice) into
-// the wave's LDS slot at the padded row pitch (8-byte aligned: two b64 stores).
+// LDS offset, within the wave's slot, of piece q of a unit: pieces
+// [0, kMainPieces) are row q / kCols, bytes 16 (q % kCols) of the row's main
+// slice; for split layouts the next 32 (Q5) are the rows' qh slices and the
+// last 32 the scale slices (row i / 2, half i % 2).
 template <int QT>
 __device__ __forceinline__ int piece_lds(int q) {
     using U = Unit<QT>;
-    if constexpr (U::kSplit) {
-        if (q < 128) return (q >> 3) * U::kPitch + 16 * (q & 7);                  // qs
-        const int i = q - 128;
-        if (U::kQ5 && i < 32) return (i >> 1) * U::kPitch + U::kQhOff + 16 * (i & 1);  // qh
-        const int j = U::kQ5 ? i - 32 : i;
-        return (j >> 1) * U::kPitch + U::kScOff + 16 * (j & 1);                  // scales
-    } else {
+    if (!U::kSplit || q < U::kMainPieces) {
         const int r = q / U::kCols, c = q - U::kCols * r;
         return r * U::kPitch + 16 * c;
     }
+    const int i = q - U::kMainPieces;
+    if (U::kQ5 && i < 32) return (i >> 1) * U::kPitch + U::kQhOff + 16 * (i & 1);
+    const int j = U::kQ5 ? i - 32 : i;
+    return (j >> 1) * U::kPitch + U::kScOff + 16 * (j & 1);
 }
 
 template <int QT>
@@ -189,11 +217,11 @@ template <int QT>
 __device__ __forceinline__ PairLane pair_lane(int lane) {
     constexpr int BB = Fmt<QT>::kBlockBytes;
     const int G = lane >> 4, bp = G >> 1, h = G & 1;
-    if constexpr (Unit<QT>::kSplit) {  // offsets within pair 0; pairs step 32 / 8 / 8 bytes
+    if constexpr (Unit<QT>::kSplit) {  // offsets within pair 0; pairs step 2 kQsBytes / 8 / 8 bytes
         PairLane pl;
         pl.bp = bp;
         pl.h = h;
-        pl.qoff = 16 * bp + 8 * h;
+        pl.qoff = Fmt<QT>::kQsBytes * bp + 8 * h;
         pl.sh = 0u;
         pl.hoff = Unit<QT>::kQhOff + 4 * bp;
         pl.doff = Unit<QT>::kScOff + 4 * bp;
@@ -201,7 +229,7 @@ __device__ __forceinline__ PairLane pair_lane(int lane) {
         return pl;
     }
     const int o = BB * bp;                  // the block's first byte within the pair
-    const int qs = o + (BB - 16) + 8 * h;   // the lane's first qs byte
+    const int qs = o + (BB - Fmt<QT>::kQsBytes) + 8 * h;   // the lane's first qs byte
     PairLane pl;
     pl.bp = bp;
     pl.h = h;
@@ -231,26 +259,34 @@ __device__ __forceinline__ float chunk_dot_x(const uint8_t* rowd, const PairLane
                                              const float* xs, float acc) {
     using U = Unit<QT>;
     constexpr int NP = NB / 2;
-    // pair strides: GGUF blocks are interleaved records; split planes step 32 (qs), 8 (qh, scales)
-    constexpr int PQ = U::kSplit ? 32 : 2 * Fmt<QT>::kBlockBytes;
+    // pair strides: GGUF blocks are interleaved records; split planes step 2 kQsBytes (qs), 8 (qh, scales)
+    constexpr int PQ = U::kSplit ? 2 * U::kQsPerBlock : 2 * Fmt<QT>::kBlockBytes;
     constexpr int PH = U::kSplit ? 8 : PQ;
     v4i bq[NP];
     uint32_t sc[NP];
+    // 8 bytes of the lane's block at byte offset off of the pair (dword aligned base, shift pl.sh)
+    auto read8 = [&](const uint8_t* b, uint32_t* lo, uint32_t* hi) {
+        if constexpr (U::kSplit) {
+            *lo = *reinterpret_cast<const uint32_t*>(b);
+            *hi = *reinterpret_cast<const uint32_t*>(b + 4);
+        } else {
+            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(b);
+            const uint32_t w1 = *reinterpret_cast<const uint32_t*>(b + 4);
+            const uint32_t w2 = *reinterpret_cast<const uint32_t*>(b + 8);
+            *lo = __builtin_amdgcn_alignbyte(w1, w0, pl.sh);
+            *hi = __builtin_amdgcn_alignbyte(w2, w1, pl.sh);
+        }
+    };
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
         const uint8_t* pq = rowd + PQ * p + pl.qoff;
         uint32_t qa, qb;  // qs bytes 8h..8h+3 and 8h+4..8h+7 of the lane's block
-        if constexpr (U::kSplit) {
-            qa = *reinterpret_cast<const uint32_t*>(pq);
-            qb = *reinterpret_cast<const uint32_t*>(pq + 4);
-        } else {
-            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(pq);
-            const uint32_t w1 = *reinterpret_cast<const uint32_t*>(pq + 4);
-            const uint32_t w2 = *reinterpret_cast<const uint32_t*>(pq + 8);
-            qa = __builtin_amdgcn_alignbyte(w1, w0, pl.sh);
-            qb = __builtin_amdgcn_alignbyte(w2, w1, pl.sh);
-        }
-        if constexpr (!U::kQ5) {
+        read8(pq, &qa, &qb);
+        if constexpr (U::kQ8) {
+            uint32_t qc, qd;  // int8 weights at positions 16+8h..16+8h+7
+            read8(pq + 16, &qc, &qd);
+            bq[p] = (v4i){(int)qa, (int)qb, (int)qc, (int)qd};
+        } else if constexpr (!U::kQ5) {
             const long la = pack_q4(qa), lb = pack_q4(qb);  // (lo | hi << 32) of each dword
             bq[p] = (v4i){(int)(uint32_t)la, (int)(uint32_t)lb, (int)(uint32_t)(la >> 32), (int)(uint32_t)(lb >> 32)};
         } else {
@@ -329,8 +365,8 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     __shared__ float red[NW];
     const int nb = K >> 5;
     const int nu = nb / kUnitBlocks;  // units per tile
-    // GGUF: one record plane of kBB bytes per block; split: qs 16, qh 4, scales 4 bytes per block
-    const uint32_t row_bytes = (uint32_t)nb * (uint32_t)(U::kSplit ? 16 : U::kBB);
+    // main plane bytes per row (GGUF records, or the split qs plane); split qh / scale planes 4 per block
+    const uint32_t row_bytes = (uint32_t)nb * (uint32_t)U::kMainPerBlock;
     const uint32_t row_bytes4 = (uint32_t)nb * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int G = gridDim.x;
@@ -346,22 +382,19 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     float* xscale = reinterpret_cast<float*>(xdig + nb * kXStride);
     float* part = xscale + nb;  // [my_tiles][NW][16]
 
-    // This lane's three 16-byte pieces of a unit: piece q = row q / kCols,
-    // bytes 16 (q % kCols) of the row's slice.  Rows past M fall beyond the
-    // buffer and load zeros.
-    // Split layouts: loads 0-1 are qs pieces (row q / 8, bytes 16 (q % 8) of the row's 128-byte
-    // qs slice); load 2 of lanes 0-31 (Q5: lanes 32-63 too) reads 16 bytes of a row's 32-byte qh
-    // or scale slice (row i / 2, half i % 2).
-    uint32_t poff[3];
+    // This lane's 16-byte pieces of a unit: piece q = lane + 64 k (see piece_lds).
+    // Main-plane pieces past the unit (GGUF tails) are clamped to its last piece
+    // and not parked; rows past M fall beyond the buffer and load zeros.
+    uint32_t poff[U::kLoads];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const int q = min(lane + 64 * k, U::kPieces - 1);
-        if constexpr (U::kSplit) {
-            const int i = (q >= 128 ? q - 128 : q) & 31;
-            poff[k] = q < 128 ? (uint32_t)(q >> 3) * row_bytes + 16u * (uint32_t)(q & 7)
-                              : (uint32_t)(i >> 1) * row_bytes4 + 16u * (uint32_t)(i & 1);
+    for (int k = 0; k < U::kLoads; ++k) {
+        const int q = lane + 64 * k;
+        if (!U::kSplit || q < U::kMainPieces) {
+            const int qc = min(q, U::kMainPieces - 1);
+            poff[k] = (uint32_t)(qc / U::kCols) * row_bytes + 16u * (uint32_t)(qc % U::kCols);
         } else {
-            poff[k] = (uint32_t)(q / U::kCols) * row_bytes + 16u * (uint32_t)(q % U::kCols);
+            const int i = (q - U::kMainPieces) & 31;  // row i / 2, half i % 2 of a qh or scale slice
+            poff[k] = (uint32_t)(i >> 1) * row_bytes4 + 16u * (uint32_t)(i & 1);
         }
     }
     // unit s of the stream -> (tile slot i, unit u)
@@ -369,22 +402,22 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         const int i = s / max(per_w, 1);
         const int u = wave + NW * (s - i * per_w);
         const uint32_t row0 = (uint32_t)(((int)blockIdx.x + G * i) * 16);
-        const uint32_t base = s < L ? row0 * row_bytes + (uint32_t)u * (U::kSplit ? 128u : (uint32_t)U::kRowBytes)
-                                    : kPastEnd;
-        if constexpr (U::kSplit) {
-            const uint32_t base4 = s < L ? row0 * row_bytes4 + (uint32_t)u * 32u : kPastEnd;
-            buf[0] = buf_load_b128(wr, s < L ? base + poff[0] : kPastEnd);
-            buf[1] = buf_load_b128(wr, s < L ? base + poff[1] : kPastEnd);
-            const uint32_t o2 = s < L ? base4 + poff[2] : kPastEnd;
-            if (U::kQ5 ? lane < 32 : false)
-                buf[2] = buf_load_b128(hr, o2);
-            else if (U::kQ5 || lane < 32)
-                buf[2] = buf_load_b128(sr, o2);
-            else
-                buf[2] = make_uint4(0, 0, 0, 0);
-        } else {
+        const uint32_t base = s < L ? row0 * row_bytes + (uint32_t)u * (uint32_t)U::kMainRow : kPastEnd;
+        const uint32_t base4 = s < L ? row0 * row_bytes4 + (uint32_t)u * 32u : kPastEnd;
 #pragma unroll
-            for (int k = 0; k < 3; ++k) buf[k] = buf_load_b128(wr, s < L ? base + poff[k] : kPastEnd);
+        for (int k = 0; k < U::kLoads; ++k) {
+            if (!U::kSplit || 64 * k + 63 < U::kMainPieces) {  // the whole load is main plane
+                buf[k] = buf_load_b128(wr, s < L ? base + poff[k] : kPastEnd);
+            } else {  // split tail: qh (Q5, lanes 0-31) and scale slices; no piece for the rest
+                const int q = lane + 64 * k - U::kMainPieces;
+                const uint32_t o = s < L ? base4 + poff[k] : kPastEnd;
+                if (U::kQ5 && q < 32)
+                    buf[k] = buf_load_b128(hr, o);
+                else if (q < (U::kQ5 ? 64 : 32))
+                    buf[k] = buf_load_b128(sr, o);
+                else
+                    buf[k] = make_uint4(0, 0, 0, 0);
+            }
         }
     };
 
@@ -407,7 +440,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     __builtin_amdgcn_sched_barrier(0);
 
     // 2) the first D units of this wave's stream.
-    uint4 buf[D][3];
+    uint4 buf[D][U::kLoads];
 #pragma unroll
     for (int d = 0; d < D; ++d) load_unit(buf[d], d);
     __builtin_amdgcn_sched_barrier(0);
@@ -527,7 +560,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
             for (int r = 0; r < R; ++r) {
                 const int s = s0 + r, j = r % PW, d = r % D;
 #pragma unroll
-                for (int k = 0; k < 3; ++k) {
+                for (int k = 0; k < U::kLoads; ++k) {
                     const int q = lane + 64 * k;
                     if (q < U::kPieces) park_piece<QT>(wbuf, q, buf[d][k]);
                 }
@@ -552,7 +585,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
             const int s = s0 + d;
             if (s < L) {
 #pragma unroll
-                for (int k = 0; k < 3; ++k) {
+                for (int k = 0; k < U::kLoads; ++k) {
                     const int q = lane + 64 * k;
                     if (q < U::kPieces) park_piece<QT>(wbuf, q, buf[d][k]);
                 }
@@ -623,8 +656,12 @@ int launch_nw(const Planes& pw, const float* x, float* y, int M, int K, int grid
     const int nb = K / 32;
     const int xq = (nb * 4 + NW * 64 - 1) / (NW * 64);
     if (xq <= 1) return launch_xq<QT, 1, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);
-    if (xq <= 2) return launch_xq<QT, 2, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);
-    return launch_xq<QT, 4, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);  // nb <= 512, NW >= 8: at most 4 items per thread
+    if constexpr (NW >= 16) {  // nb <= 512: at most 2 items per thread
+        return launch_xq<QT, 2, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);
+    } else {
+        if (xq <= 2) return launch_xq<QT, 2, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);
+        return launch_xq<QT, 4, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);  // NW >= 8: at most 4 items per thread
+    }
 }
 
 // Workgroup layout of one launch: grid size, tiles per workgroup, waves, LDS bytes.
@@ -676,7 +713,7 @@ template <int QT>
 bool mfma_eligible(const Planes& pw, const float* x, const MatvecOpts& o, int64_t M, int64_t K) {
     using U = Unit<QT>;
     const int64_t nb = K / 32;
-    const int64_t plane = (M + 16) * nb * (U::kSplit ? 16 : U::kBB);  // largest plane, with the last tile's padding
+    const int64_t plane = (M + 16) * nb * U::kMainPerBlock;  // largest plane, with the last tile's padding
     bool aligned = (uintptr_t)pw.w % 4 == 0;
     if (U::kSplit) aligned = (uintptr_t)pw.w % 16 == 0 && (uintptr_t)pw.wsc % 16 == 0 && (!U::kQ5 || (uintptr_t)pw.wh % 16 == 0);
     return K % 256 == 0 && nb >= kUnitBlocks && nb <= kMaxBlocks && M >= 1 && M <= INT32_MAX - 16 &&
@@ -724,18 +761,37 @@ int q5_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t
                                  MatvecOpts());
 }
 
-bool split_mfma_eligible(bool q5, const void* qs, const uint8_t* qh, const float* scales, const float* x, int64_t M,
-                         int64_t K) {
-    const Planes pw{static_cast<const uint8_t*>(qs), qh, scales};
-    return q5 ? mfma_eligible<kFmtQ5Split>(pw, x, MatvecOpts(), M, K)
-              : mfma_eligible<kFmtQ4Split>(pw, x, MatvecOpts(), M, K);
+bool q8_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& o, int64_t M, int64_t K) {
+    return mfma_eligible<kFmtQ8_0>(Planes{static_cast<const uint8_t*>(w), nullptr, nullptr}, x, o, M, K);
 }
 
-int split_mfma_launch(bool q5, const void* qs, const uint8_t* qh, const float* scales, const float* x, float* y,
+int q8_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st,
+                     const MatvecOpts& o) {
+    return mfma_launch<kFmtQ8_0>(Planes{static_cast<const uint8_t*>(w), nullptr, nullptr}, x, y, M, K, st, o);
+}
+
+bool split_mfma_eligible(int bits, const void* qs, const uint8_t* qh, const float* scales, const float* x, int64_t M,
+                         int64_t K) {
+    const Planes pw{static_cast<const uint8_t*>(qs), qh, scales};
+    const MatvecOpts o;
+    switch (bits) {
+        case 4: return mfma_eligible<kFmtQ4Split>(pw, x, o, M, K);
+        case 5: return mfma_eligible<kFmtQ5Split>(pw, x, o, M, K);
+        case 8: return mfma_eligible<kFmtQ8Split>(pw, x, o, M, K);
+        default: return false;
+    }
+}
+
+int split_mfma_launch(int bits, const void* qs, const uint8_t* qh, const float* scales, const float* x, float* y,
                       int64_t M, int64_t K, hipStream_t st) {
     const Planes pw{static_cast<const uint8_t*>(qs), qh, scales};
-    return q5 ? mfma_launch<kFmtQ5Split>(pw, x, y, M, K, st, MatvecOpts())
-              : mfma_launch<kFmtQ4Split>(pw, x, y, M, K, st, MatvecOpts());
+    const MatvecOpts o;
+    switch (bits) {
+        case 4: return mfma_launch<kFmtQ4Split>(pw, x, y, M, K, st, o);
+        case 5: return mfma_launch<kFmtQ5Split>(pw, x, y, M, K, st, o);
+        case 8: return mfma_launch<kFmtQ8Split>(pw, x, y, M, K, st, o);
+        default: return fail(kInvalidArgument, "split matvec: %d-bit planes", bits);
+    }
 }
 
 }  // namespace asmhip

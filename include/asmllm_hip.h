@@ -56,9 +56,11 @@ extern "C" {
 #define ASMHIP_PRE_RMSNORM 1 /* x <- (x * 1/sqrt(mean(x^2) + eps)) * pre_arg */
 #define ASMHIP_PRE_SWIGLU 2  /* x <- x / (1 + exp(-x)) * pre_arg             */
 
-/* Q4_0 kernel selection (asmhip_set_q4_kernel), for GGUF blocks and the split
- * layout.  The int8-MFMA stream needs K % 256 == 0, K <= 16384 and 16-byte
- * aligned x (and, for split planes, 16-byte aligned planes). */
+/* Matvec kernel selection (asmhip_set_q4_kernel): the int8-MFMA stream or the
+ * fp32 VALU kernels, for Q4_0 (GGUF and split); ASMHIP_Q4_KERNEL_FP32 also
+ * keeps Q5_0 and Q8_0 on the fp32 kernels.  The MFMA stream needs
+ * K % 256 == 0, K <= 16384 and 16-byte aligned x (and, for split planes,
+ * 16-byte aligned planes). */
 #define ASMHIP_Q4_KERNEL_AUTO 0 /* int8 MFMA kernel where eligible, else fp32             */
 #define ASMHIP_Q4_KERNEL_FP32 1 /* fp32 VALU kernel only                                   */
 #define ASMHIP_Q4_KERNEL_MFMA 2 /* int8 MFMA kernel only (GGUF shapes it cannot take:

@@ -266,6 +266,27 @@ def test_split_layout_both_kernels(hip, oracle, q4_kernel, M, K):
         assert_matvec_close(dy.download(np.float32, M), ref, w, x)
 
 
+@pytest.mark.parametrize("M,K", [(1, 256), (300, 2304), (4096, 4096), (11008, 4096), (64, 16384), (33, 2080)])
+def test_q8_gguf_and_split_both_kernels(hip, oracle, q4_kernel, M, K):
+    """Q8_0 GGUF blocks (asmhip_matmul_q8_0) and the split layout
+    (asmhip_matmul_q8_split): the int8-MFMA stream where K % 256 == 0 and the
+    fp32 VALU kernel (forced, and for K = 2080) within the bar of the oracle."""
+    blocks, x = _weights(M * 3 + K, M, K, qt="q8")
+    qs, sc = gguf.split_q8_0(blocks)
+    ref = oracle.matmul_q8_0_gguf(blocks, x, NT)
+    w = oracle.dequantize_q8_0(blocks)
+    db, dq, ds = DeviceBuffer.from_numpy(blocks), DeviceBuffer.from_numpy(qs), DeviceBuffer.from_numpy(sc)
+    dx, dy = DeviceBuffer.from_numpy(x), DeviceBuffer(M * 4)
+    for kernel in (native.Q4_KERNEL_AUTO, native.Q4_KERNEL_FP32):
+        q4_kernel(kernel)
+        assert hip.asmhip_matmul_q8_0(db.ptr, dx.ptr, dy.ptr, M, K, None) == 0, hip.asmhip_last_error()
+        synchronize()
+        assert_matvec_close(dy.download(np.float32, M), ref, w, x)
+        assert hip.asmhip_matmul_q8_split(dq.ptr, ds.ptr, dx.ptr, dy.ptr, M, K, None) == 0, hip.asmhip_last_error()
+        synchronize()
+        assert_matvec_close(dy.download(np.float32, M), ref, w, x)
+
+
 def test_bad_arguments_are_rejected(hip):
     dx, dy, db = DeviceBuffer(4096 * 4), DeviceBuffer(64 * 4), DeviceBuffer(64 * 128 * 18)
     assert hip.asmhip_matmul_q4_0(db.ptr, dx.ptr, dy.ptr, 64, 4010, None) == -1
