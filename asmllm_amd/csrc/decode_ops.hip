@@ -257,7 +257,8 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     constexpr int kRows = kAttnSplitLen / kRowPos;
     static_assert(kAttnSplitLen % kRowPos == 0, "split must hold whole rows");
     __shared__ float cs[HD];                 // cos, sin of pair i at 2i, 2i+1
-    __shared__ float wst[kBlock / kWave][HD + 2];
+    constexpr int kGroupsWg = kBlock / kLanes;  // lane groups (position slots) of the workgroup
+    __shared__ float wst[kGroupsWg][HD + 2];
 
     const int h = blockIdx.x, split = blockIdx.y, S = gridDim.y;
     const int group = n_heads / n_kv, kvh = h / group;
@@ -358,34 +359,26 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
             }
         }
     }
-    // merge the lane groups of the wave
+    // every lane group's softmax state to LDS (no cross-lane shuffles), then one
+    // merge over all groups of the workgroup in group order; thread t < HD owns
+    // dimension t of this workgroup's partial
+    {
+        const int gs = w * kGroups + g;
 #pragma unroll
-    for (int o = kLanes; o < kWave; o <<= 1) {
-        const float m2 = __shfl_xor(m, o, kWave), l2 = __shfl_xor(l, o, kWave);
-        const float M = fmaxf(m, m2);
-        const float f1 = M == -INFINITY ? 0.f : __expf(m - M), f2 = M == -INFINITY ? 0.f : __expf(m2 - M);
-        l = l * f1 + l2 * f2;
-#pragma unroll
-        for (int t = 0; t < E; ++t) acc[t] = acc[t] * f1 + __shfl_xor(acc[t], o, kWave) * f2;
-        m = M;
-    }
-    if (g == 0) {
-#pragma unroll
-        for (int t = 0; t < E; ++t) wst[w][2 + E * c + t] = acc[t];
-        if (c == 0) wst[w][0] = m, wst[w][1] = l;
+        for (int t = 0; t < E; ++t) wst[gs][2 + E * c + t] = acc[t];
+        if (c == 0) wst[gs][0] = m, wst[gs][1] = l;
     }
     __syncthreads();
-    // merge the waves; thread t < HD owns dimension t of this workgroup's partial
     float* mine = part + ((size_t)h * S + split) * (HD + 2);
     if (threadIdx.x < HD) {
         float M = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < kBlock / kWave; ++i) M = fmaxf(M, wst[i][0]);
+        for (int i = 0; i < kGroupsWg; ++i) M = fmaxf(M, wst[i][0]);
         float L = 0.f, a = 0.f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int i = 0; i < kBlock / kWave; ++i) {
-                const float f = __expf(wst[i][0] - M);
+            for (int i = 0; i < kGroupsWg; ++i) {
+                const float f = __expf(wst[i][0] - M);  // 0 for groups that saw no position
                 L = fmaf(wst[i][1], f, L);
                 a = fmaf(wst[i][2 + threadIdx.x], f, a);
             }
