@@ -1,8 +1,13 @@
-// Q4_0 GGUF matvec on the int8 matrix cores of gfx950.
+// Quantized matvec on the int8 matrix cores of gfx950.
 //
-// y[m] = sum_b d[m,b] * sum_j (n[m,b,j] - 8) * x[32b + j]
-// (the reference's asm_matmul_q4, src/kernels/x86_64/matmul_q4_avx2.asm:57-287,
-// over GGUF blocks read in place).
+// y[m] = sum_b d[m,b] * sum_j w[m,b,j] * x[32b + j], with w = n - 8 (Q4_0),
+// (n | bit << 4) - 16 (Q5_0) or q (Q8_0): the reference's asm_matmul_q4 /
+// asm_matmul_q5 / asm_matmul_q8 (src/kernels/x86_64/matmul_q4_avx2.asm:57-287,
+// matmul_q5_avx2.asm:52-238, matmul_q8_avx2.asm:51-194), over GGUF blocks read
+// in place or over the reference's split qs / qh / fp32-scale planes.  The
+// block format is a template parameter (Fmt / Unit below); the description
+// that follows uses Q4_0, the other formats differ only in how a lane builds
+// its weight bytes and in the x scale.
 //
 // One v_mfma_i32_16x16x64_i8 per (16 rows, block pair 2p, 2p+1):
 //   B operand  lane (n, G), n the weight row, G the k-group: groups 0-1 take
