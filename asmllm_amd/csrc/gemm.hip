@@ -286,12 +286,19 @@ __global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* _
         loff[i] = live ? (uint32_t)(r * S::kPitch + 16 * k) : (uint32_t)(S::kRows * S::kPitch);
     }
     uint4 pre[D][S::kPerThread];
+    // A's pieces end at piece 64 kPieces, a multiple of 64, and NTH is a multiple
+    // of 64, so every wave's slot i is all A or all W: the choice of buffer is
+    // wave-uniform (made scalar here; a per-lane choice of descriptor would turn
+    // every load into a waterfall loop).
+    bool a_wave[S::kPerThread];
+#pragma unroll
+    for (int i = 0; i < S::kPerThread; ++i) a_wave[i] = __builtin_amdgcn_readfirstlane((int)is_a[i]) != 0;
     auto fetch = [&](uint4* dst, int kb0) {
         const uint32_t kofs = (uint32_t)kb0 * 34u;
 #pragma unroll
         for (int i = 0; i < S::kPerThread; ++i) {
             const uint32_t off = goff[i] == kPastEnd ? kPastEnd : goff[i] + kofs;
-            dst[i] = buf_load_b128(is_a[i] ? ar : wr, off);
+            dst[i] = buf_load_b128(a_wave[i] ? ar : wr, off);
         }
     };
     auto park = [&](const uint4* src, uint8_t* stage) {
