@@ -500,6 +500,21 @@ extern "C" int asmhip_matmul_fused(int qtype, const void* blocks, const float* x
     return matvec_launch(qt, true, blocks, nullptr, x, y, M, K, (hipStream_t)stream, o);
 }
 
+extern "C" int asmhip_matmul_swiglu(int qtype, const void* blocks, const float* x, float* h, int64_t H, int64_t K,
+                                    int pre_op, const float* pre_arg, float eps, float* work, void* stream) {
+    QuantType qt;
+    int rc = check_ptrs(blocks, x, h);
+    if (!rc) rc = quant_type(qtype, &qt);
+    if (rc) return rc;
+    MatvecOpts o;
+    o.pre = pre_op;
+    o.pre_arg = pre_arg;
+    o.eps = eps;
+    if (o.pre != kPreNone && !o.pre_arg) return fail(kInvalidArgument, "matvec_swiglu: pre-op without its argument");
+    if (o.pre < kPreNone || o.pre > kPreSwiGlu) return fail(kInvalidArgument, "matvec_swiglu: unknown pre-op %d", o.pre);
+    return matvec_swiglu_launch(qt, blocks, x, h, H, K, work, (hipStream_t)stream, o);
+}
+
 extern "C" int asmhip_gemm_q8_0(const void* w_blocks, const void* a_blocks, float* c, int64_t T, int64_t M,
                                 int64_t K, void* stream) {
     int rc = check_ptrs(w_blocks, a_blocks, c);

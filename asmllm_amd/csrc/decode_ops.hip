@@ -6,6 +6,7 @@
 //   rope           rope_avx2.asm:52-146          interleaved pairs (2p, 2p+1), freq = theta^(-2p/hd)
 //   softmax        softmax_avx2.asm:48-130       max, exp(x - max), / sum
 //   silu_hadamard  swiglu_avx2.asm:45-81         gate = gate / (1 + exp(-gate)) * up
+//   swiglu_pairs   the same product over gate/up values interleaved in groups of 8
 //   attention      attention_avx2.asm:59-218     softmax(q k^T * scale) v, all rows (non-causal)
 //
 // plus the device-side pieces of the decode engine: RoPE fused with the fp16
@@ -147,6 +148,16 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 __global__ __launch_bounds__(kBlock) void silu_kernel(float* __restrict__ g, const float* __restrict__ u, int dim) {
     const int i = blockIdx.x * kBlock + threadIdx.x;
     if (i < dim) g[i] = silu_mul(g[i], u[i]);
+}
+
+// gate/up rows interleaved in groups of 8: output j pairs entries 16 (j / 8) + j % 8 and + 8
+__global__ __launch_bounds__(kBlock) void swiglu_pairs_kernel(const float* __restrict__ gu, float* __restrict__ h,
+                                                              int H) {
+    const int j = blockIdx.x * kBlock + threadIdx.x;
+    if (j < H) {
+        const int i = 16 * (j >> 3) + (j & 7);
+        h[j] = silu_mul(gu[i], gu[i + 8]);
+    }
 }
 
 // ---- reference attention: one workgroup per query row, scores in LDS ----------------
@@ -522,6 +533,14 @@ int rope_kv_write_launch(float* qkv, void* k_cache, void* v_cache, int n_heads, 
 int softmax_launch(const float* x, float* y, int64_t dim, hipStream_t st) {
     if (dim <= 0 || dim > INT32_MAX) return fail(kInvalidArgument, "softmax: bad dim");
     hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(1024), 0, st, x, y, (int)dim);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int swiglu_pairs_launch(const float* gu, float* h, int64_t H, hipStream_t st) {
+    if (H <= 0 || H % 8 || H > INT32_MAX / 2) return fail(kInvalidArgument, "swiglu: need H > 0 and H %% 8 == 0");
+    hipLaunchKernelGGL(swiglu_pairs_kernel, dim3((unsigned)((H + kBlock - 1) / kBlock)), dim3(kBlock), 0, st, gu, h,
+                       (int)H);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

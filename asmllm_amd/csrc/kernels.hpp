@@ -18,11 +18,20 @@ enum PreOp : int {
     kPreSwiGlu = 2,   // x <- x / (1 + exp(-x)) * arg[k]
 };
 
+// Work fused into a matvec's write of y.  kPostSwiGlu8: the rows of W come in
+// groups of 16, the first 8 gate rows and the next 8 the matching up rows, and
+// y[8 g + r] = silu(row 16 g + r) * row 16 g + 8 + r (M / 2 outputs).
+enum PostOp : int {
+    kPostNone = 0,
+    kPostSwiGlu8 = 1,
+};
+
 struct MatvecOpts {
     int pre = kPreNone;
     const float* pre_arg = nullptr;
     float eps = 0.f;
     bool accumulate = false;  // y += W x
+    int post = kPostNone;
 };
 
 // y = W x.  gguf: W is [M][K/32] GGUF blocks; otherwise W is the split qs
@@ -86,6 +95,15 @@ int rope_kv_write_launch(float* qkv, void* k_cache, void* v_cache, int n_heads, 
                          const int* pos_ptr, int max_ctx, float theta, hipStream_t st);
 int softmax_launch(const float* x, float* y, int64_t dim, hipStream_t st);
 int silu_launch(float* g, const float* u, int64_t dim, hipStream_t st);
+// h[8 g + r] = silu(gu[16 g + r]) * gu[16 g + 8 + r] for j < H (H % 8 == 0):
+// kPostSwiGlu8 as its own launch over a matvec's 2H outputs.
+int swiglu_pairs_launch(const float* gu, float* h, int64_t H, hipStream_t st);
+// h = silu(W_gate x) * (W_up x) over GGUF blocks whose 2H rows interleave gate
+// and up in groups of 8 (kPostSwiGlu8), x transformed by o.pre on the way in.
+// One launch where the int8-MFMA stream takes the shape; otherwise the matvec
+// writes its 2H outputs to `work` and swiglu_pairs_launch combines them.
+int matvec_swiglu_launch(QuantType qt, const void* w, const float* x, float* h, int64_t H, int64_t K, float* work,
+                         hipStream_t st, const MatvecOpts& o);
 int attention_launch(const float* q, const float* k, const float* v, float* y, int64_t seq, int64_t hd, float scale,
                      hipStream_t st);
 

@@ -638,6 +638,7 @@ int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, c
     if (M > INT32_MAX || K > INT32_MAX) return fail(kInvalidArgument, "matvec: M and K must fit in int32");
     if (opts.pre != kPreNone && !opts.pre_arg) return fail(kInvalidArgument, "matvec: pre-op without its argument");
     if (opts.pre < kPreNone || opts.pre > kPreSwiGlu) return fail(kInvalidArgument, "matvec: unknown pre-op %d", opts.pre);
+    if (opts.post != kPostNone) return fail(kInvalidArgument, "matvec: post-ops go through matvec_swiglu_launch");
     const int64_t nb = K / 32;
     const int64_t blk_bytes = qt == QuantType::Q4_0 ? (gguf ? 18 : 16) : (gguf ? 34 : 32);
     const int64_t total = M * nb * blk_bytes;
@@ -736,6 +737,25 @@ int dequant_launch(QuantType qt, const void* w, float* out, int64_t rows, int64_
                            static_cast<const uint8_t*>(w), out, nblocks);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
+}
+
+int matvec_swiglu_launch(QuantType qt, const void* w, const float* x, float* h, int64_t H, int64_t K, float* work,
+                         hipStream_t stream, const MatvecOpts& opts) {
+    if (H <= 0 || H % 8 || H > INT32_MAX / 4)
+        return fail(kInvalidArgument, "matvec_swiglu: need H > 0 and H %% 8 == 0 (got H=%lld)", (long long)H);
+    if (opts.accumulate || opts.post != kPostNone)
+        return fail(kInvalidArgument, "matvec_swiglu: the output is overwritten, no other post-op");
+    if (!work) return fail(kInvalidArgument, "matvec_swiglu: null work buffer");
+    MatvecOpts po = opts;
+    po.post = kPostSwiGlu8;
+    const int64_t M = 2 * H;
+    if (g_q4_kernel.load(std::memory_order_relaxed) != kQ4KernelFp32) {
+        if (qt == QuantType::Q4_0 && q4_0_mfma_eligible(w, x, po, M, K)) return q4_0_mfma_launch(w, x, h, M, K, stream, po);
+        if (qt == QuantType::Q8_0 && q8_0_mfma_eligible(w, x, po, M, K)) return q8_0_mfma_launch(w, x, h, M, K, stream, po);
+    }
+    // any other shape or kernel: the 2H rows to `work`, then the pairs combined
+    const int rc = matvec_launch(qt, true, w, nullptr, x, work, M, K, stream, opts);
+    return rc ? rc : swiglu_pairs_launch(work, h, H, stream);
 }
 
 int q5_matvec_launch(bool gguf, const void* w, const uint8_t* qh, const float* scales, const float* x, float* y,

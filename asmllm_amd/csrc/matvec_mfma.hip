@@ -47,7 +47,8 @@
 // unit w), a wave loads its A operands and block scales into registers once
 // and reuses them for every tile, which takes the x reads out of the per-unit
 // LDS traffic.  Each wave keeps its per-tile partial sums in LDS; after the
-// stream the workgroup adds the NW partials of every row in a fixed order.
+// stream the workgroup adds the NW partials of every row in a fixed order
+// (kPostSwiGlu8: a tile's 8 gate and 8 up rows leave as 8 silu(gate) * up).
 // The main loop has no workgroup barrier.
 #include <algorithm>
 
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
                                                             const float* __restrict__ wsc,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int M, int K, int pre, const float* __restrict__ pre_arg,
-                                                            float eps, int accumulate) {
+                                                            float eps, int accumulate, int post) {
     using U = Unit<QT>;
     constexpr int kThreads = NW * 64;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -613,6 +614,21 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     __syncthreads();
 
     // 5) add the waves' partial sums of every row in a fixed order.
+    if (post == kPostSwiGlu8) {
+        // a tile is 8 gate rows and their 8 up rows (M % 16 == 0): y[8 tile + r] = silu(gate) * up
+        for (int idx = threadIdx.x; idx < my_tiles * 8; idx += kThreads) {
+            const int i = idx >> 3, r = idx & 7;
+            const int tile = (int)blockIdx.x + G * i;
+            float gs = 0.f, us = 0.f;
+#pragma unroll
+            for (int k = 0; k < NW; ++k) {
+                gs += part[(i * NW + k) * 16 + r];
+                us += part[(i * NW + k) * 16 + 8 + r];
+            }
+            y[tile * 8 + r] = __fmul_rn(gs / (1.0f + expf(-gs)), us);
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < my_tiles * 16; idx += kThreads) {
         const int i = idx >> 4, r = idx & 15;
         const int row = ((int)blockIdx.x + G * i) * 16 + r;
@@ -650,7 +666,7 @@ int launch_xq(const Planes& pw, const float* x, float* y, int M, int K, int grid
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
     hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW>), dim3(grid), dim3(NW * 64), lds, st, pw.w, pw.wh,
-                       pw.wsc, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate);
+                       pw.wsc, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate, o.post);
     return kOk;
 }
 
@@ -724,6 +740,7 @@ bool mfma_eligible(const Planes& pw, const float* x, const MatvecOpts& o, int64_
     return K % 256 == 0 && nb >= kUnitBlocks && nb <= kMaxBlocks && M >= 1 && M <= INT32_MAX - 16 &&
            plane < (int64_t)kPastEnd && aligned && (uintptr_t)x % 16 == 0 &&
            (o.pre == kPreNone || (uintptr_t)o.pre_arg % 16 == 0) &&
+           (o.post == kPostNone || (M % 16 == 0 && !o.accumulate && !U::kSplit)) &&
            stream_shape(U::kSlotBytes, M, K).lds <= kLdsBudget;
 }
 

@@ -8,11 +8,13 @@ matvec + residual, RMSNorm, gate/up matvecs, SiLU*up, down matvec + residual]
 native calls.  Here the same sequence is a fixed list of launches on one
 stream, so it can be captured once into a HIP graph and replayed per token:
 
-  * q, k and v weights are stacked into one [q; k; v] Q4_0 matrix and gate/up
-    into one [gate; up] matrix (rows are independent, so y is the same as
-    three or two separate matvecs); the RMSNorms are fused into the read of x
-    by the matvec that follows them, SiLU*up into the down matvec's read, and
-    both residual adds into the o and down matvecs (accumulate);
+  * q, k and v weights are stacked into one [q; k; v] Q4_0 matrix (rows are
+    independent, so y is the same as three separate matvecs), and gate/up
+    into one matrix whose rows interleave the two in groups of 8, so that one
+    matvec launch also forms silu(gate) * up as it writes its outputs
+    (asmhip_matmul_swiglu); the RMSNorms are fused into the read of x by the
+    matvec that follows them, and both residual adds into the o and down
+    matvecs (accumulate);
   * the token id and the position live in device ints: the embedding kernel
     reads the token, RoPE / the KV write / attention read the position, and
     the argmax kernel writes the next token and advances the position, so a
@@ -22,8 +24,8 @@ stream, so it can be captured once into a HIP graph and replayed per token:
   * the KV cache is fp16, head-major [n_kv_heads][max_ctx][head_dim] per layer
     (the reference keeps fp32 [128][heads][head_dim], generate.py:252-253);
   * head_dim 48 (the reference's stories15M demo model, dim 288), 64 or 128;
-    where dim or hidden_dim is not a multiple of 64 the RMSNorm / SwiGLU runs
-    as its own launch before the matvec instead of inside it.
+    where dim is not a multiple of 64 the RMSNorm runs as its own launch
+    before the matvec instead of inside it.
 
 All weights are Q4_0 GGUF blocks, including the token embedding and the
 lm-head (generate.py:182-184 loads both through get_tensor).
@@ -110,6 +112,24 @@ def shape_from_gguf(g) -> LlamaShape:
                       theta=float(get("rope.freq_base", 10000.0)))
 
 
+def interleave_gate_up(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """[gate; up] block rows ([H][nb][bytes] each, H % 8 == 0) in the order
+    asmhip_matmul_swiglu reads them: 8 gate rows, then the same 8 up rows."""
+    if gate.shape != up.shape or gate.shape[0] % 8:
+        raise ValueError(f"gate {gate.shape} / up {up.shape}: need equal shapes and a multiple of 8 rows")
+    H = gate.shape[0]
+    g = gate.reshape(H // 8, 1, 8, *gate.shape[1:])
+    u = up.reshape(H // 8, 1, 8, *up.shape[1:])
+    return np.concatenate([g, u], axis=1).reshape(2 * H, *gate.shape[1:])
+
+
+def split_gate_up(gu: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Inverse of interleave_gate_up."""
+    H = gu.shape[0] // 2
+    v = gu.reshape(H // 8, 2, 8, *gu.shape[1:])
+    return v[:, 0].reshape(H, *gu.shape[1:]), v[:, 1].reshape(H, *gu.shape[1:])
+
+
 class _Layer:
     def __init__(self, s: LlamaShape, max_ctx: int):
         d, h = s.dim, s.hidden_dim
@@ -157,12 +177,12 @@ class DecodeEngine:
         self.x = DeviceBuffer(4 * s.dim)
         self.qkv = DeviceBuffer(4 * s.qkv_rows)
         self.attn = DeviceBuffer(4 * s.dim)
-        self.gu = DeviceBuffer(4 * 2 * s.hidden_dim)
+        self.gu = DeviceBuffer(4 * 2 * s.hidden_dim)  # work buffer of asmhip_matmul_swiglu
+        self.ffn = DeviceBuffer(4 * s.hidden_dim)     # silu(gate) * up
         self.logits = DeviceBuffer(4 * s.vocab)
-        # The matvecs fuse RMSNorm / SwiGLU into their read of x when K % 64 == 0;
-        # otherwise (stories15M: dim 288) the op runs as its own launch first.
+        # The matvecs fuse RMSNorm into their read of x when K % 64 == 0;
+        # otherwise (stories15M: dim 288) it runs as its own launch first.
         self.fuse_norm = s.dim % 64 == 0
-        self.fuse_swiglu = s.hidden_dim % 64 == 0
         self.xn = None if self.fuse_norm else DeviceBuffer(4 * s.dim)
         ws = self.lib.asmhip_attention_decode_workspace(s.n_heads, s.head_dim, self.max_ctx)
         self.workspace = DeviceBuffer(4 * max(int(ws), 1))
@@ -205,8 +225,14 @@ class DecodeEngine:
         ly.ffn_norm.upload(np.asarray(ffn_norm, np.float32))
         ly.wqkv.upload(np.concatenate([wq, wk, wv], axis=0))
         ly.wo.upload(wo)
-        ly.wgu.upload(np.concatenate([w_gate, w_up], axis=0))
+        ly.wgu.upload(interleave_gate_up(np.asarray(w_gate), np.asarray(w_up)))
         ly.wdown.upload(w_down)
+
+    def gate_up_blocks(self, i: int) -> tuple[np.ndarray, np.ndarray]:
+        """The gate and up matrices of layer i as host GGUF blocks [hidden_dim][dim/32][18]."""
+        s = self.shape
+        gu = self.layers[i].wgu.download(np.uint8, (2 * s.hidden_dim, s.dim // 32, 18))
+        return split_gate_up(gu)
 
     def load_globals(self, *, embed, final_norm, output) -> None:
         """Token embedding and lm-head as host GGUF blocks of the engine's
@@ -288,17 +314,20 @@ class DecodeEngine:
         s, L, st = self.shape, self.lib, self.stream.handle
         d, h, hd = s.dim, s.hidden_dim, s.head_dim
         eps = ctypes.c_float(s.eps)
-        Q4, RMS, SWI, NONE = native.Q4_0, native.PRE_RMSNORM, native.PRE_SWIGLU, native.PRE_NONE
+        Q4, RMS, NONE = native.Q4_0, native.PRE_RMSNORM, native.PRE_NONE
 
         def mv(w, x, y, M, K, pre, arg, acc, what, qtype=Q4):
             check(L.asmhip_matmul_fused(qtype, w.ptr, x, y, M, K, pre, arg, eps, acc, st), what)
 
-        def normed(norm, M, w, y, what, qtype=Q4):  # y = W rmsnorm(x; norm)
+        def norm_in(norm):  # (x, pre-op, argument) that give the matvec rmsnorm(x; norm)
             if self.fuse_norm:
-                mv(w, self.x.ptr, y, M, d, RMS, norm.ptr, 0, what, qtype)
-            else:
-                check(L.asmhip_rmsnorm(self.x.ptr, norm.ptr, self.xn.ptr, d, eps, st), "rmsnorm")
-                mv(w, self.xn.ptr, y, M, d, NONE, None, 0, what, qtype)
+                return self.x.ptr, RMS, norm.ptr
+            check(L.asmhip_rmsnorm(self.x.ptr, norm.ptr, self.xn.ptr, d, eps, st), "rmsnorm")
+            return self.xn.ptr, NONE, None
+
+        def normed(norm, M, w, y, what, qtype=Q4):  # y = W rmsnorm(x; norm)
+            xin, pre, arg = norm_in(norm)
+            mv(w, xin, y, M, d, pre, arg, 0, what, qtype)
 
         embed = L.asmhip_embed_q8_0 if self.embed_type == native.Q8_0 else L.asmhip_embed_q4_0
         check(embed(self.embed.ptr, self.token.ptr, self.x.ptr, s.vocab, d, st), "embed")
@@ -308,12 +337,10 @@ class DecodeEngine:
                                                  self.attn.ptr, s.n_heads, s.n_kv_heads, hd, self.pos.ptr,
                                                  self.max_ctx, ctypes.c_float(s.theta), st), "rope + attention")
             mv(ly.wo, self.attn.ptr, self.x.ptr, d, d, NONE, None, 1, "o matvec")
-            normed(ly.ffn_norm, 2 * h, ly.wgu, self.gu.ptr, "gate/up matvec")
-            if self.fuse_swiglu:
-                mv(ly.wdown, self.gu.ptr, self.x.ptr, d, h, SWI, self.gu.ptr + 4 * h, 1, "down matvec")
-            else:
-                check(L.asmhip_silu_hadamard(self.gu.ptr, self.gu.ptr + 4 * h, h, st), "silu * up")
-                mv(ly.wdown, self.gu.ptr, self.x.ptr, d, h, NONE, None, 1, "down matvec")
+            xin, pre, arg = norm_in(ly.ffn_norm)
+            check(L.asmhip_matmul_swiglu(Q4, ly.wgu.ptr, xin, self.ffn.ptr, h, d, pre, arg, eps, self.gu.ptr, st),
+                  "gate/up matvec + swiglu")
+            mv(ly.wdown, self.ffn.ptr, self.x.ptr, d, h, NONE, None, 1, "down matvec")
         normed(self.final_norm, s.vocab, self.output, self.logits.ptr, "lm-head matvec", self.output_type)
         check(L.asmhip_argmax(self.logits.ptr, s.vocab, self.token.ptr, self.pos.ptr, st), "argmax")
 

@@ -56,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_dequantize_q4_0": (c_int, [_P, _P, c_int64, c_int64, _P]),
     "asmhip_dequantize_q8_0": (c_int, [_P, _P, c_int64, c_int64, _P]),
     "asmhip_matmul_fused": (c_int, [c_int, _P, _P, _P, c_int64, c_int64, c_int, _P, c_float, c_int, _P]),
+    "asmhip_matmul_swiglu": (c_int, [c_int, _P, _P, _P, c_int64, c_int64, c_int, _P, c_float, _P, _P]),
     "asmhip_gemm_q8_0": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, _P]),
     "asmhip_set_q4_kernel": (c_int, [c_int]),
     "asmhip_get_q4_kernel": (c_int, []),

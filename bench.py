@@ -385,12 +385,12 @@ def decode_cpu_baseline(eng, context: int, seconds: float) -> dict:
         return buf.download(np.uint8, (rows, K // 32, 18))
 
     layers, kcs, vcs = [], [], []
-    for ly in eng.layers:
-        qkv, gu = blocks(ly.wqkv, s.qkv_rows, d), blocks(ly.wgu, 2 * h, d)
+    for i, ly in enumerate(eng.layers):
+        qkv, (gate, up) = blocks(ly.wqkv, s.qkv_rows, d), eng.gate_up_blocks(i)
         layers.append({"attn_norm": ly.attn_norm.download(np.float32, d),
                        "ffn_norm": ly.ffn_norm.download(np.float32, d),
                        "wq": qkv[:d], "wk": qkv[d:d + kv], "wv": qkv[d + kv:], "wo": blocks(ly.wo, d, d),
-                       "w_gate": gu[:h], "w_up": gu[h:], "w_down": blocks(ly.wdown, d, h)})
+                       "w_gate": gate, "w_up": up, "w_down": blocks(ly.wdown, d, h)})
         kcs.append(ly.k_cache.download(np.uint16, (s.n_kv_heads, eng.max_ctx, s.head_dim)))
         vcs.append(ly.v_cache.download(np.uint16, (s.n_kv_heads, eng.max_ctx, s.head_dim)))
     cores = host_cores()

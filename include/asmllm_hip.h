@@ -160,6 +160,16 @@ ASMHIP_API int asmhip_dequantize_q5_0(const void* blocks, float* w, int64_t rows
  * != 0 adds W x into y (the residual add) instead of overwriting y. */
 ASMHIP_API int asmhip_matmul_fused(int qtype, const void* blocks, const float* x, float* y, int64_t M, int64_t K,
                                    int pre_op, const float* pre_arg, float eps, int accumulate, void* stream);
+/* The FFN's gate/up matvecs and silu(gate) * up in one call (generate.py:308-313
+ * computes them as two matvecs and asm_silu_hadamard, swiglu_avx2.asm:45-81):
+ * blocks holds 2H rows that interleave the gate and up matrices in groups of 8
+ * (rows 16g..16g+7 = gate rows 8g..8g+7, rows 16g+8..16g+15 = up rows 8g..8g+7;
+ * H % 8 == 0), and h[j] = gate_j / (1 + exp(-gate_j)) * up_j, with x
+ * transformed by pre_op as in asmhip_matmul_fused.  work: 2H floats of device
+ * memory, written only where the int8-MFMA stream cannot take the shape (the
+ * matvec then writes its 2H outputs there and a second launch combines them). */
+ASMHIP_API int asmhip_matmul_swiglu(int qtype, const void* blocks, const float* x, float* h, int64_t H, int64_t K,
+                                    int pre_op, const float* pre_arg, float eps, float* work, void* stream);
 /* Prefill GEMM: C[T][M] = sum over blocks b of int32 dot(A[t,b], W[j,b]) * d_w[j,b] * d_a[t,b],
  * accumulated in fp32 in block order; A = T activation rows and W = M weight rows, both
  * Q8_0 blocks [rows][K/32] (quantize activations with asmhip_quantize(ASMHIP_Q8_0, ...)).

@@ -29,13 +29,13 @@ def _oracle_model(eng: DecodeEngine, nt: int):
     s = eng.shape
     d, h, kv = s.dim, s.hidden_dim, s.kv_dim
     layers, kcs, vcs = [], [], []
-    for ly in eng.layers:
+    for i, ly in enumerate(eng.layers):
         qkv = _blocks(ly.wqkv, s.qkv_rows, d)
-        gu = _blocks(ly.wgu, 2 * h, d)
+        gate, up = eng.gate_up_blocks(i)
         layers.append({
             "attn_norm": ly.attn_norm.download(np.float32, d), "ffn_norm": ly.ffn_norm.download(np.float32, d),
             "wq": qkv[:d], "wk": qkv[d:d + kv], "wv": qkv[d + kv:],
-            "wo": _blocks(ly.wo, d, d), "w_gate": gu[:h], "w_up": gu[h:], "w_down": _blocks(ly.wdown, d, h),
+            "wo": _blocks(ly.wo, d, d), "w_gate": gate, "w_up": up, "w_down": _blocks(ly.wdown, d, h),
         })
         shape = (s.n_kv_heads, eng.max_ctx, s.head_dim)
         kcs.append(ly.k_cache.download(np.uint16, shape))

@@ -72,3 +72,22 @@ def test_7b_decode_byte_budget():
     assert LLAMA_7B.weight_bytes() == 3_716_481_024
     assert LLAMA_7B.kv_bytes_per_position() == 524_288
     assert LLAMA_7B.head_dim == 128 and LLAMA_7B.qkv_rows == 3 * 4096
+
+
+def test_gate_up_interleave_round_trip():
+    """The engine's gate/up row order (8 gate rows, the same 8 up rows, ...)."""
+    from asmllm_amd.engine import interleave_gate_up, split_gate_up
+
+    rng = np.random.default_rng(3)
+    gate = rng.integers(0, 256, (24, 3, 18), dtype=np.uint8)
+    up = rng.integers(0, 256, (24, 3, 18), dtype=np.uint8)
+    gu = interleave_gate_up(gate, up)
+    assert gu.shape == (48, 3, 18)
+    for g in range(3):
+        np.testing.assert_array_equal(gu[16 * g:16 * g + 8], gate[8 * g:8 * g + 8])
+        np.testing.assert_array_equal(gu[16 * g + 8:16 * g + 16], up[8 * g:8 * g + 8])
+    g2, u2 = split_gate_up(gu)
+    np.testing.assert_array_equal(g2, gate)
+    np.testing.assert_array_equal(u2, up)
+    with pytest.raises(ValueError):
+        interleave_gate_up(gate[:20], up[:20])

@@ -395,6 +395,76 @@ def test_fused_matvec(hip, oracle, q4_kernel, qt, kernel, pre, accumulate):
         assert_matvec_close(y, ref, w, x_eff)
 
 
+# ---- gate/up matvec with silu(gate) * up formed as it writes y ------------------------------
+
+def _swiglu(hip, qtype, gu, x, pre, arg, eps):
+    H, K = gu.shape[0] // 2, gu.shape[1] * 32
+    db, dx = DeviceBuffer.from_numpy(gu), DeviceBuffer.from_numpy(x)
+    da = DeviceBuffer.from_numpy(arg) if arg is not None else None
+    dh, work = DeviceBuffer(H * 4), DeviceBuffer(2 * H * 4)
+    rc = hip.asmhip_matmul_swiglu(qtype, db.ptr, dx.ptr, dh.ptr, H, K, pre, da.ptr if da else None, eps, work.ptr,
+                                  None)
+    assert rc == 0, hip.asmhip_last_error()
+    synchronize()
+    return dh.download(np.float32, H)
+
+
+@pytest.mark.parametrize("qt,kernel,H,K,pre", [
+    ("q4", native.Q4_KERNEL_AUTO, 5504, 4096, "rmsnorm"),   # the 7B FFN: one MFMA-stream launch
+    ("q4", native.Q4_KERNEL_FP32, 5504, 4096, "rmsnorm"),   # fp32 kernel into work, then the pairs kernel
+    ("q4", native.Q4_KERNEL_AUTO, 768, 288, "none"),        # stories15M: K = 288 is no MFMA-stream shape
+    ("q4", native.Q4_KERNEL_AUTO, 1000, 2048, "none"),      # 125 tiles, the general (K != 4096) stream
+    ("q8", native.Q4_KERNEL_AUTO, 1000, 4096, "none"),
+], ids=["q4-7b-mfma", "q4-7b-fp32", "q4-k288", "q4-k2048", "q8"])
+def test_matmul_swiglu(hip, oracle, q4_kernel, qt, kernel, H, K, pre):
+    from asmllm_amd.engine import interleave_gate_up
+
+    q4_kernel(kernel)
+    gate, x = _weights(31 + H, H, K, qt)
+    up, _ = _weights(77 + H, H, K, qt)
+    gu = interleave_gate_up(gate, up)
+    rng = np.random.default_rng(H)
+    arg, x_eff, code = None, x, native.PRE_NONE
+    if pre == "rmsnorm":
+        arg = rng.uniform(0.5, 1.5, K).astype(np.float32)
+        x_eff, code = oracle.rmsnorm(x, arg, 1e-6), native.PRE_RMSNORM
+    qtype = native.Q4_0 if qt == "q4" else native.Q8_0
+    h = _swiglu(hip, qtype, gu, x, code, arg, 1e-6)
+
+    # exactly the two-step result on the GPU: the same 2H rows without the
+    # epilogue, de-interleaved, then asmhip_silu_hadamard
+    y = _fused(hip, qtype, gu, x, code, arg, 1e-6, None).reshape(H // 8, 2, 8)
+    dg, du = DeviceBuffer.from_numpy(y[:, 0].reshape(H)), DeviceBuffer.from_numpy(y[:, 1].reshape(H))
+    assert hip.asmhip_silu_hadamard(dg.ptr, du.ptr, H, None) == 0, hip.asmhip_last_error()
+    synchronize()
+    np.testing.assert_array_equal(h, dg.download(np.float32, H))
+
+    # and the reference's sequence (two matvecs, silu_hadamard) within the matvec bar
+    # carried through silu(g) u: |d/dg| <= 1.1 |u|, |d/du| = |silu(g)|
+    mv, dq = ((oracle.matmul_q4_0_gguf, oracle.dequantize_q4_0) if qt == "q4"
+              else (oracle.matmul_q8_0_gguf, oracle.dequantize_q8_0))
+    g_ref, u_ref = mv(gate, x_eff, NT), mv(up, x_eff, NT)
+    h_ref = oracle.silu_hadamard(g_ref, u_ref).astype(np.float64)
+    ax = np.abs(x_eff.astype(np.float64))
+    l1g, l1u = np.abs(dq(gate).astype(np.float64)) @ ax, np.abs(dq(up).astype(np.float64)) @ ax
+    silu = np.abs(h_ref / np.where(u_ref == 0, 1, u_ref))
+    bound = 1.1 * np.abs(u_ref) * 1e-4 * l1g + silu * 1e-4 * l1u + 4 * 2.0 ** -23 * np.abs(h_ref) + 1e-30
+    assert np.all(np.abs(h.astype(np.float64) - h_ref) <= bound)
+
+
+def test_matmul_swiglu_rejects_bad_arguments(hip):
+    blocks, x = _weights(9, 32, 4096)
+    db, dx, dh, work = (DeviceBuffer.from_numpy(blocks), DeviceBuffer.from_numpy(x), DeviceBuffer(16 * 4),
+                        DeviceBuffer(32 * 4))
+    f = hip.asmhip_matmul_swiglu
+    assert f(native.Q4_0, db.ptr, dx.ptr, dh.ptr, 12, 4096, 0, None, 0.0, work.ptr, None) == -1  # H % 8
+    assert f(native.Q4_0, db.ptr, dx.ptr, dh.ptr, 16, 4096, 0, None, 0.0, None, None) == -1      # no work
+    assert f(native.Q4_0, db.ptr, dx.ptr, dh.ptr, 16, 4096, native.PRE_RMSNORM, None, 1e-6, work.ptr, None) == -1
+    assert f(5, db.ptr, dx.ptr, dh.ptr, 16, 4096, 0, None, 0.0, work.ptr, None) == -1
+    assert f(native.Q4_0, db.ptr, dx.ptr, dh.ptr, 16, 4096, 0, None, 0.0, work.ptr, None) == 0
+    synchronize()
+
+
 def test_fused_pre_op_needs_its_argument(hip):
     blocks, x = _weights(9, 16, 4096)
     db, dx, dy = DeviceBuffer.from_numpy(blocks), DeviceBuffer.from_numpy(x), DeviceBuffer(16 * 4)
