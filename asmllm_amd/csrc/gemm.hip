@@ -19,8 +19,9 @@
 // matrix pipe keeps the VALU at two instructions per output and block, the
 // bound of this GEMM: every output needs its own scale in every block.
 //
-// Work mapping: a workgroup of 4 waves computes a 64 (T) x 128 (M) tile; wave
-// (wt, wm) owns rows 32 wt.. and columns 64 wm.. (two 32x32 tiles).
+// Work mapping: a workgroup computes a 64 (T) x 128 (M) tile, as 8 waves of
+// one 32x32 tile on the coalesced path below (4 waves of two on the general
+// path: wave (wt, wm) owns rows 32 wt.. and columns 64 wm..).
 // Fast path (K % 64 == 0): K goes in steps of two blocks; a row's step is 68
 // contiguous bytes, fetched with 16-byte loads by consecutive lanes and parked
 // raw in LDS (row pitch an odd number of dwords: conflict-free operand reads),
@@ -334,24 +335,32 @@ __global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* _
             if (s + D < nsteps) fetch(pre[u], (s + D) * KB);
             const uint8_t* arow = stage + (32 * wt + m) * S::kPitch;
             const uint8_t* wrow = stage + (kTT + 32 * WT * wm + m) * S::kPitch;
-            // block BLK (0 or 1) of the dword-aligned pair at byte 68 bp
+            // block BLK (0 or 1) of the dword-aligned pair at byte 68 bp: operands,
+            // then the matrix instructions back to back, then the epilogue
             auto block = [&](auto blk_c, int bp) {
                 constexpr int BLK = decltype(blk_c)::value;
                 const uint8_t* ar_ = arow + 68 * bp;
                 const v4i av = raw_qs<BLK>(ar_, g);
                 const v4h da = raw_scale<BLK>(ar_);
+                v4i bv[WT];
+                v4h dw[WT];
+#pragma unroll
+                for (int nt = 0; nt < WT; ++nt) {
+                    const uint8_t* w_ = wrow + 32 * nt * S::kPitch + 68 * bp;
+                    bv[nt] = raw_qs<BLK>(w_, g);
+                    dw[nt] = raw_scale<BLK>(w_);
+                }
+                __builtin_amdgcn_sched_barrier(0);
                 const v16i zi = {};
                 const v16f zf = {};
                 v16i dd[WT];
                 v16f ss[WT];
 #pragma unroll
                 for (int nt = 0; nt < WT; ++nt) {
-                    const uint8_t* w_ = wrow + 32 * nt * S::kPitch + 68 * bp;
-                    const v4i bv = raw_qs<BLK>(w_, g);
-                    const v4h dw = raw_scale<BLK>(w_);
-                    dd[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zi, 0, 0, 0);
-                    ss[nt] = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw, zf, 0, 0, 0);  // 2 d_a d_w
+                    dd[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[nt], zi, 0, 0, 0);
+                    ss[nt] = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw[nt], zf, 0, 0, 0);  // 2 d_a d_w
                 }
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int nt = 0; nt < WT; ++nt)
 #pragma unroll
@@ -379,10 +388,11 @@ __global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* _
 
 // Two blocks per staged K step, one step of loads in flight per thread.
 // Deeper register rings (2-4 steps) and 4- or 8-block steps measured slower on
-// MI355X: the extra registers cost occupancy.
+// MI355X: the extra registers cost occupancy.  So did issuing both blocks'
+// matrix instructions before either epilogue (194 VGPRs with two tiles a wave).
 constexpr int kGemmKB = 2;  // blocks per staged K step (even)
 constexpr int kGemmD = 1;   // K steps of loads in flight per thread
-constexpr int kGemmWT = 2;  // 32-column tiles per wave (8 waves of one tile measured 6% slower)
+constexpr int kGemmWT = 1;  // 32-column tiles per wave: 8 waves of one tile (4 of two measured 4% slower)
 
 }  // namespace
 
