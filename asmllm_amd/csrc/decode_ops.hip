@@ -198,9 +198,10 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(const float* __restri
 // positions [s*kAttnSplitLen, (s+1)*kAttnSplitLen) of 0..pos.  Within a workgroup
 // a position is read by HD/8 lanes (8 dims = 16 bytes each), so a wave covers
 // 64/(HD/8) positions per row and the four waves kRowPos; every k and v load of
-// the workgroup is issued before the first score is formed.  Each lane group
-// keeps a softmax state (max m, sum l, acc[8]) over its positions; the states
-// merge across lane groups (shuffles) and waves (LDS); each workgroup writes
+// the workgroup is issued before the first score is formed (q, then every k
+// row, then every v row).  Each lane group keeps a softmax state (max m, sum l,
+// acc[8]) over its positions; the states of all lane groups of the workgroup
+// merge once through LDS; each workgroup writes
 // [m, l, acc[HD]] to `part`, and attn_decode_merge combines the S partials of a
 // head in split order into out = acc / l.
 //
@@ -255,6 +256,8 @@ struct HalfRow {
     }
 };
 
+constexpr uint32_t kAttnPastEnd = 0xFFFFFF00u;  // buffer offset that loads zeros
+
 template <int HD, bool ROPE>
 __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __restrict__ qkv, __half* kc, __half* vc,
                                                              float* __restrict__ part, int n_heads, int n_kv,
@@ -280,26 +283,40 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     const int g = lane / kLanes, c = lane % kLanes;
     const size_t head_off = (size_t)kvh * max_ctx * HD + E * c;
 
-    // all k and v rows of this lane, issued up front
-    // all k rows first, then all v rows: the scores can start while v is in flight
-    HalfRow<E> kr[kRows], vr[kRows];
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        const int p = p0 + r * kRowPos + w * kGroups + g;
-        const bool live = p < p1 && !(ROPE && p == pos);
-        kr[r] = live ? HalfRow<E>::load(kc + head_off + (size_t)p * HD) : HalfRow<E>::zero();
-    }
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        const int p = p0 + r * kRowPos + w * kGroups + g;
-        const bool live = p < p1 && !(ROPE && p == pos);
-        vr[r] = live ? HalfRow<E>::load(vc + head_off + (size_t)p * HD) : HalfRow<E>::zero();
-    }
+    // q first, then all k rows of this lane, then all v rows: loads return in
+    // order, so the scores can start while v is in flight.  HD % 64 == 0:
+    // branch-free buffer loads, a row outside the split reading zeros from past
+    // the end of the buffer.
     float qv[E];
 #pragma unroll
     for (int t = 0; t < E; t += 2) {
         const float2 a = *reinterpret_cast<const float2*>(qkv + (size_t)h * HD + E * c + t);
         qv[t] = a.x, qv[t + 1] = a.y;
+    }
+    HalfRow<E> kr[kRows], vr[kRows];
+    const uint32_t cache_bytes = (uint32_t)n_kv * (uint32_t)max_ctx * (uint32_t)(2 * HD);  // < 4 GB, checked at launch
+    const auto kres = make_rsrc(kc, cache_bytes), vres = make_rsrc(vc, cache_bytes);
+    uint32_t off[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        const int p = p0 + r * kRowPos + w * kGroups + g;
+        const bool live = p < p1 && !(ROPE && p == pos);
+        off[r] = live ? 2u * (uint32_t)(head_off + (size_t)p * HD) : kAttnPastEnd;
+        if constexpr (E == 8) {
+            const uint4 a = buf_load_b128(kres, off[r]);
+            kr[r].w[0] = a.x, kr[r].w[1] = a.y, kr[r].w[2] = a.z, kr[r].w[3] = a.w;
+        } else {
+            kr[r] = live ? HalfRow<E>::load(kc + head_off + (size_t)p * HD) : HalfRow<E>::zero();
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        if constexpr (E == 8) {
+            const uint4 b = buf_load_b128(vres, off[r]);
+            vr[r].w[0] = b.x, vr[r].w[1] = b.y, vr[r].w[2] = b.z, vr[r].w[3] = b.w;
+        } else {
+            vr[r] = off[r] != kAttnPastEnd ? HalfRow<E>::load(vc + off[r] / 2) : HalfRow<E>::zero();
+        }
     }
     if constexpr (ROPE) {
         if (threadIdx.x < HD / 2 && n_pos > 0)
@@ -574,11 +591,14 @@ int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx) {
 int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* part, float* out, int n_heads,
                        int n_kv, int hd, const int* pos_ptr, int max_ctx, bool rope, float theta, hipStream_t st) {
     if (n_kv <= 0 || n_heads % n_kv) return fail(kInvalidArgument, "attention: n_heads %% n_kv_heads != 0");
+    if (max_ctx <= 0) return fail(kInvalidArgument, "attention: max_ctx must be > 0");
     const int splits = attn_decode_splits(max_ctx);
     if (splits > 64)
         return fail(kUnsupported, "attention: max_ctx %d exceeds %d positions", max_ctx, 64 * kAttnSplitLen);
     if ((uintptr_t)qkv % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
         return fail(kInvalidArgument, "attention: q and the caches must be 16-byte aligned");
+    if ((int64_t)n_kv * max_ctx * hd * 2 >= (int64_t)kAttnPastEnd)
+        return fail(kUnsupported, "attention: caches of 4 GB or more per layer are not supported");
     const dim3 grid(n_heads, splits);
     __half* kc = (__half*)k_cache;
     __half* vc = (__half*)v_cache;
