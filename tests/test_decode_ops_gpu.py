@@ -118,12 +118,25 @@ def test_multi_head_rope_reads_position_on_device(hip, oracle):
             np.testing.assert_allclose(gk[h], rk, rtol=TOL, atol=TOL)
 
 
+def _random_attention_cases(n, seed):
+    """Seeded random head layouts, cache lengths and positions."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        hd = int(rng.choice([48, 64, 128]))
+        n_kv = int(rng.choice([1, 2, 4, 8]))
+        n_heads = n_kv * int(rng.choice([1, 2, 4]))
+        max_ctx = int(rng.integers(1, 4097))
+        cases.append((n_heads, n_kv, hd, int(rng.integers(0, max_ctx)), max_ctx))
+    return cases
+
+
 @pytest.mark.parametrize("n_heads,n_kv,hd,pos,max_ctx", [
     (32, 32, 128, 0, 256), (32, 32, 128, 2047, 2176), (32, 8, 128, 700, 1024), (8, 2, 64, 129, 130),
     (32, 8, 128, 128, 300), (4, 4, 128, 127, 128), (8, 8, 64, 8191, 8192),
     # head_dim 48 (stories15M): one split, several, and 64 splits (more than the merge's 48 threads)
     (6, 6, 48, 5, 64), (6, 6, 48, 300, 2048), (6, 2, 48, 8000, 8192),
-])
+] + _random_attention_cases(8, 77))
 def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos, max_ctx):
     rng = np.random.default_rng(n_heads * 1000 + pos)
     qkv = rng.standard_normal((n_heads + 2 * n_kv) * hd).astype(np.float32)

@@ -175,6 +175,28 @@ def test_ragged_shapes(hip, oracle, qt, M, K):
         assert_matvec_close(y, oracle.matmul_q8_0_gguf(blocks, x), oracle.dequantize_q8_0(blocks), x)
 
 
+def _sweep_cases(n, seed):
+    """Seeded random (qt, M, K): M in [1, 6000], K a multiple of 32 up to 12800,
+    about half of them multiples of 256 (the shapes the MFMA stream takes)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        M = int(rng.integers(1, 6001))
+        K = 256 * int(rng.integers(1, 51)) if i % 2 == 0 else 32 * int(rng.integers(1, 401))
+        cases.append(("q4" if i % 3 else "q8", M, K))
+    return cases
+
+
+@pytest.mark.parametrize("qt,M,K", _sweep_cases(24, 2024))
+def test_random_shape_sweep(hip, oracle, qt, M, K):
+    blocks, x = _weights(M + 13 * K, M, K, qt)
+    y = _gguf_matvec(hip, qt, blocks, x)
+    if qt == "q4":
+        assert_matvec_close(y, oracle.matmul_q4_0_gguf(blocks, x, NT), oracle.dequantize_q4_0(blocks), x)
+    else:
+        assert_matvec_close(y, oracle.matmul_q8_0_gguf(blocks, x, NT), oracle.dequantize_q8_0(blocks), x)
+
+
 def test_all_eight_nibbles_give_zero(hip):
     blocks = np.zeros((64, 128, 18), np.uint8)
     blocks[..., 0:2] = np.array([0.37], np.float16).view(np.uint8)
@@ -450,6 +472,23 @@ def test_matmul_swiglu(hip, oracle, q4_kernel, qt, kernel, H, K, pre):
     silu = np.abs(h_ref / np.where(u_ref == 0, 1, u_ref))
     bound = 1.1 * np.abs(u_ref) * 1e-4 * l1g + silu * 1e-4 * l1u + 4 * 2.0 ** -23 * np.abs(h_ref) + 1e-30
     assert np.all(np.abs(h.astype(np.float64) - h_ref) <= bound)
+
+
+@pytest.mark.parametrize("H,K", [(8, 256), (24, 4096), (1000, 768), (2048, 2560), (4096, 8192), (136, 96)])
+def test_matmul_swiglu_shapes(hip, H, K):
+    """Bitwise the two-step result (matvec of the same rows, then asmhip_silu_hadamard)
+    at shapes from one tile to several tiles per workgroup, MFMA stream and not."""
+    from asmllm_amd.engine import interleave_gate_up
+
+    gate, x = _weights(5 + H + K, H, K)
+    up, _ = _weights(9 + H + K, H, K)
+    gu = interleave_gate_up(gate, up)
+    h = _swiglu(hip, native.Q4_0, gu, x, native.PRE_NONE, None, 0.0)
+    y = _fused(hip, native.Q4_0, gu, x, native.PRE_NONE, None, 0.0, None).reshape(H // 8, 2, 8)
+    dg, du = DeviceBuffer.from_numpy(y[:, 0].reshape(H)), DeviceBuffer.from_numpy(y[:, 1].reshape(H))
+    assert hip.asmhip_silu_hadamard(dg.ptr, du.ptr, H, None) == 0, hip.asmhip_last_error()
+    synchronize()
+    np.testing.assert_array_equal(h, dg.download(np.float32, H))
 
 
 def test_matmul_swiglu_rejects_bad_arguments(hip):
