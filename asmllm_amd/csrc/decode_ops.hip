@@ -469,18 +469,19 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
     __shared__ int bi[16];
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    // 8 elements per thread and pass, all loaded before any is compared (one
-    // memory round per 8192 logits instead of one per 1024); within a thread
-    // indices rise, so strict > keeps the first maximum
-    for (int base = 0; base < n; base += 8 * 1024) {
-        float x[8];
+    // 32 elements per thread and pass, all loaded before any is compared (one
+    // memory round per 32768 logits: a single pass for a 32000-token vocabulary);
+    // within a thread indices rise, so strict > keeps the first maximum
+    constexpr int kPer = 32;
+    for (int base = 0; base < n; base += kPer * 1024) {
+        float x[kPer];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < kPer; ++k) {
             const int i = base + k * 1024 + (int)threadIdx.x;
             x[k] = i < n ? logits[i] : -INFINITY;
         }
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < kPer; ++k) {
             const int i = base + k * 1024 + (int)threadIdx.x;
             if (x[k] > v) {
                 v = x[k];

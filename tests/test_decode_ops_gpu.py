@@ -216,6 +216,22 @@ def test_embed_row_and_argmax(hip, oracle):
     assert int(dpos.download(np.int32, 1)[0]) == 42
 
 
+@pytest.mark.parametrize("n", [1, 5, 1024, 32000, 32768, 32769, 128256])
+def test_argmax_sizes_and_ties(hip, n):
+    """One pass (n <= 32768) and several (the Llama-3 vocabulary); a tie across
+    passes and lanes resolves to the first index, as numpy.argmax."""
+    rng = np.random.default_rng(n)
+    logits = rng.standard_normal(n).astype(np.float32)
+    if n > 2:
+        a, b = sorted(rng.choice(n, 2, replace=False))
+        logits[[a, b]] = 9.0
+    dl = DeviceBuffer.from_numpy(logits)
+    dtok = DeviceBuffer.from_numpy(np.array([-1], np.int32))
+    _ok(hip, hip.asmhip_argmax(dl.ptr, n, dtok.ptr, None, None))
+    synchronize()
+    assert int(dtok.download(np.int32, 1)[0]) == int(np.argmax(logits))
+
+
 # ---- GPU quantizers and synthetic weights -----------------------------------------------------
 
 @pytest.mark.parametrize("qt", ["q4", "q8"])
