@@ -440,7 +440,8 @@ __global__ __launch_bounds__(HD) void attn_decode_merge(const float* __restrict_
             a = fmaf(ph[(size_t)i * (HD + 2) + 2 + threadIdx.x], f, a);
         }
     }
-    out[(size_t)h * HD + threadIdx.x] = a / L;
+    // no position in range (pos outside [0, max_ctx)): a defined zero instead of 0 / 0
+    out[(size_t)h * HD + threadIdx.x] = M == -INFINITY ? 0.f : a / L;
 }
 
 // ---- embedding row of a Q4_0 table -----------------------------------------------------
@@ -463,15 +464,22 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(const uint8_t* __restrict
 }
 
 // ---- greedy argmax (first index of the maximum, as numpy.argmax) -------------------------
+// numpy.argmax order: a NaN ranks above every number, and equal values (NaN or
+// not) go to the lower index.
+__device__ __forceinline__ bool argmax_better(float a, int ia, float b, int ib) {
+    const bool na = a != a, nb = b != b;
+    if (na || nb) return na && (!nb || ia < ib);
+    return a > b || (a == b && ia < ib);
+}
+
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
                                                       int* __restrict__ token, int* __restrict__ pos) {
     __shared__ float bv[16];
     __shared__ int bi[16];
     float v = -INFINITY;
-    int idx = 0x7fffffff;
+    int idx = 0x7fffffff;  // padding: loses to every real element, -inf included
     // 32 elements per thread and pass, all loaded before any is compared (one
-    // memory round per 32768 logits: a single pass for a 32000-token vocabulary);
-    // within a thread indices rise, so strict > keeps the first maximum
+    // memory round per 32768 logits: a single pass for a 32000-token vocabulary)
     constexpr int kPer = 32;
     for (int base = 0; base < n; base += kPer * 1024) {
         float x[kPer];
@@ -483,7 +491,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int i = base + k * 1024 + (int)threadIdx.x;
-            if (x[k] > v) {
+            if (i < n && argmax_better(x[k], i, v, idx)) {
                 v = x[k];
                 idx = i;
             }
@@ -493,7 +501,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
     for (int o = 32; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(v, o, kWave);
         const int oi = __shfl_xor(idx, o, kWave);
-        if (ov > v || (ov == v && oi < idx)) {
+        if (argmax_better(ov, oi, v, idx)) {
             v = ov;
             idx = oi;
         }
@@ -508,7 +516,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
         float best = bv[0];
         int bidx = bi[0];
         for (int i = 1; i < 16; ++i)
-            if (bv[i] > best || (bv[i] == best && bi[i] < bidx)) {
+            if (argmax_better(bv[i], bi[i], best, bidx)) {
                 best = bv[i];
                 bidx = bi[i];
             }

@@ -651,8 +651,8 @@ int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, c
 
     int rc = kOk;
 
+    const int sel = g_q4_kernel.load(std::memory_order_relaxed);
     if (qt == QuantType::Q4_0 && gguf) {
-        const int sel = g_q4_kernel.load(std::memory_order_relaxed);
         const bool mfma_ok = q4_0_mfma_eligible(w, x, opts, M, K);
         if (sel == kQ4KernelMfma && !mfma_ok)
             return fail(kUnsupported, "matvec: the MFMA Q4_0 kernel needs K %% 256 == 0, K <= 16384, "
@@ -664,7 +664,7 @@ int matvec_launch(QuantType qt, bool gguf, const void* w, const float* scales, c
         g_q4_kernel.load(std::memory_order_relaxed) != kQ4KernelFp32 &&
         split_mfma_eligible(4, w, nullptr, scales, x, M, K))
         return split_mfma_launch(4, w, nullptr, scales, x, y, M, K, stream);
-    if (qt == QuantType::Q8_0 && g_q4_kernel.load(std::memory_order_relaxed) != kQ4KernelFp32) {
+    if (qt == QuantType::Q8_0 && sel != kQ4KernelFp32) {
         if (gguf && q8_0_mfma_eligible(w, x, opts, M, K)) return q8_0_mfma_launch(w, x, y, M, K, stream, opts);
         if (!gguf && opts.pre == kPreNone && !opts.accumulate && split_mfma_eligible(8, w, nullptr, scales, x, M, K))
             return split_mfma_launch(8, w, nullptr, scales, x, y, M, K, stream);
@@ -749,7 +749,8 @@ int matvec_swiglu_launch(QuantType qt, const void* w, const float* x, float* h, 
     MatvecOpts po = opts;
     po.post = kPostSwiGlu8;
     const int64_t M = 2 * H;
-    if (g_q4_kernel.load(std::memory_order_relaxed) != kQ4KernelFp32) {
+    const int sel = g_q4_kernel.load(std::memory_order_relaxed);
+    if (sel != kQ4KernelFp32) {
         if (qt == QuantType::Q4_0 && q4_0_mfma_eligible(w, x, po, M, K)) return q4_0_mfma_launch(w, x, h, M, K, stream, po);
         if (qt == QuantType::Q8_0 && q8_0_mfma_eligible(w, x, po, M, K)) return q8_0_mfma_launch(w, x, h, M, K, stream, po);
     }
@@ -773,7 +774,8 @@ int q5_matvec_launch(bool gguf, const void* w, const uint8_t* qh, const float* s
     const bool pairs = nb % 2 == 0 && aligned && lds <= 160 * 1024 - 256 && total < (int64_t)UINT32_MAX;
     const int m = (int)M, k = (int)K;
     int rc = kOk;
-    const bool mfma = g_q4_kernel.load(std::memory_order_relaxed) != kQ4KernelFp32;
+    const int sel = g_q4_kernel.load(std::memory_order_relaxed);
+    const bool mfma = sel != kQ4KernelFp32;
     if (mfma && gguf && q5_0_mfma_eligible(w, x, M, K)) return q5_0_mfma_launch(w, x, y, M, K, stream);
     if (mfma && !gguf && split_mfma_eligible(5, w, qh, scales, x, M, K))
         return split_mfma_launch(5, w, qh, scales, x, y, M, K, stream);

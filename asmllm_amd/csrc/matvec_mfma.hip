@@ -498,12 +498,17 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         const int it = (int)threadIdx.x + kThreads * i;
         const float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
                             xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
-        // the 4 items of a block sit in 4 consecutive lanes
-        float mx = 0.f;
+        // the 4 items of a block sit in 4 consecutive lanes.  The block maximum
+        // is taken over the bit patterns of |x|: NaN and infinities sort above
+        // every finite value, so a block holding one gets a NaN scale below and
+        // the rows it touches come out NaN (no extra reduction for the check).
+        uint32_t mb = 0u;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) mx = fmaxf(mx, fabsf(v[t]));
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+        for (int t = 0; t < 8; ++t) mb = max(mb, __float_as_uint(v[t]) & 0x7FFFFFFFu);
+        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1, 64));
+        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 2, 64));
+        const bool finite = mb < 0x7F800000u;
+        const float mx = __uint_as_float(finite ? mb : 0u);
         int e;
         frexpf(mx, &e);  // mx < 2^e (e = 0 for mx = 0)
         e = max(e, -60);
@@ -534,7 +539,8 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
                 base[4 * (4 + k)] = d2l[3 - k];
                 base[4 * (4 + k) + 2] = d2h[3 - k];
             }
-            if (g == 0) xscale[b] = ldexpf(1.0f, e - Fmt<QT>::kXScaleShift);  // 2^(e-30) for X1, / 16 or 8 for the weight bytes
+            if (g == 0)  // 2^(e-30) for X1, / 16 or 8 for the weight bytes
+                xscale[b] = finite ? ldexpf(1.0f, e - Fmt<QT>::kXScaleShift) : __builtin_nanf("");
         }
     }
     __syncthreads();

@@ -5,7 +5,10 @@ step for step, with the two storage choices of the GPU engine made explicit:
 the KV cache holds fp16 values (k after RoPE and v, rounded to nearest even
 when written), head-major [n_kv_heads][max_ctx][head_dim]; and heads may be
 grouped (n_heads / n_kv_heads query heads per kv head; the reference has
-n_heads == n_kv_heads).  Every arithmetic step calls an oracle function that
+n_heads == n_kv_heads).  ``kv_dtype="f32"`` keeps the cache in fp32 as the
+reference does (generate.py:252-253), and ``attention="f64"`` evaluates the
+per-head QK^T/sqrt(hd) -> softmax -> PV in float64 over either cache, so the
+two storage choices can be compared with nothing else changed.  Every arithmetic step calls an oracle function that
 tests/test_oracle.py pins on its own:
 
   * matvecs: oracle_matmul_q4_0_gguf (matmul_q4_avx2.asm:110-178 over GGUF
@@ -30,16 +33,22 @@ class DecodeRef:
     uint16 bits (stored position-major in k_caches / v_caches)."""
 
     def __init__(self, *, dim, n_heads, n_kv_heads, hidden_dim, vocab, eps, theta, embed, final_norm, output,
-                 layers, k_caches, v_caches, nt: int = 1):
+                 layers, k_caches, v_caches, nt: int = 1, kv_dtype: str = "f16", attention: str = "oracle"):
         self.dim, self.n_heads, self.n_kv_heads = dim, n_heads, n_kv_heads
         self.hidden_dim, self.vocab, self.eps, self.theta = hidden_dim, vocab, eps, theta
         self.hd = dim // n_heads
         self.embed, self.final_norm, self.output = embed, final_norm, output
         self.layers = layers            # dicts: attn_norm wq wk wv wo ffn_norm w_gate w_up w_down
+        if kv_dtype not in ("f16", "f32") or attention not in ("oracle", "f64"):
+            raise ValueError(f"kv_dtype {kv_dtype!r} / attention {attention!r}")
+        if kv_dtype == "f32" and attention == "oracle":
+            raise ValueError("the oracle's decode attention reads an fp16 cache; use attention='f64'")
+        self.kv_dtype, self.attention = kv_dtype, attention
         # kept position-major [max_ctx][n_kv][hd], the oracle kernel's layout, so a
-        # step slices the cache without copying it
-        self.k_caches = [np.ascontiguousarray(np.asarray(k, np.uint16).transpose(1, 0, 2)) for k in k_caches]
-        self.v_caches = [np.ascontiguousarray(np.asarray(v, np.uint16).transpose(1, 0, 2)) for v in v_caches]
+        # step slices the cache without copying it (fp16 as uint16 bits, or fp32)
+        store = np.uint16 if kv_dtype == "f16" else np.float32
+        self.k_caches = [np.ascontiguousarray(np.asarray(k, store).transpose(1, 0, 2)) for k in k_caches]
+        self.v_caches = [np.ascontiguousarray(np.asarray(v, store).transpose(1, 0, 2)) for v in v_caches]
         self.nt = nt
 
     def _mv(self, blocks, x):
@@ -53,6 +62,25 @@ class DecodeRef:
         for h in range(n):
             out[h], _ = o.rope(out[h], out[h], self.hd, self._pos, self.theta)
         return out.reshape(-1)
+
+    def _store(self, vals: np.ndarray) -> np.ndarray:
+        return vals.astype(np.float16).view(np.uint16) if self.kv_dtype == "f16" else vals.astype(np.float32)
+
+    def _attend(self, q: np.ndarray, kc: np.ndarray, vc: np.ndarray, n_pos: int) -> np.ndarray:
+        """Per query head: softmax(q . K^T / sqrt(hd)) . V over positions 0..n_pos-1
+        (generate.py:291-296); query head h reads kv head h // (n_heads / n_kv_heads)."""
+        if self.attention == "oracle":
+            return o.attention_decode_f16(q, kc, vc, n_pos, self.n_kv_heads, self.nt)
+        def wide(c):
+            return (c.view(np.float16) if self.kv_dtype == "f16" else c).astype(np.float64)
+        K, V = wide(kc[:n_pos]), wide(vc[:n_pos])               # [pos][n_kv][hd]
+        group = self.n_heads // self.n_kv_heads
+        out = np.empty((self.n_heads, self.hd), np.float64)
+        for h in range(self.n_heads):
+            s = K[:, h // group] @ q[h].astype(np.float64) / np.sqrt(self.hd)
+            p = np.exp(s - s.max())
+            out[h] = (p / p.sum()) @ V[:, h // group]
+        return out.astype(np.float32)
 
     def forward_token(self, token_id: int, pos: int) -> np.ndarray:
         """Logits of token_id at pos; writes cache row pos (generate.py:261-326)."""
@@ -68,10 +96,9 @@ class DecodeRef:
             q = self._rope_heads(q, nh)                                           # :282-285
             k = self._rope_heads(k, nkv)
             kc, vc = self.k_caches[li], self.v_caches[li]                         # :289-290
-            kc[pos] = k.reshape(nkv, hd).astype(np.float16).view(np.uint16)
-            vc[pos] = v.reshape(nkv, hd).astype(np.float16).view(np.uint16)
-            attn = o.attention_decode_f16(q.reshape(nh, hd), kc[:pos + 1], vc[:pos + 1], pos + 1, nkv,
-                                          self.nt)                                # :291-296
+            kc[pos] = self._store(k.reshape(nkv, hd))
+            vc[pos] = self._store(v.reshape(nkv, hd))
+            attn = self._attend(q.reshape(nh, hd), kc, vc, pos + 1)               # :291-296
             x = x + self._mv(ly["wo"], attn.reshape(-1))                          # :298-300
             xn = o.rmsnorm(x, ly["ffn_norm"], self.eps)                           # :302-306
             gate = self._mv(ly["w_gate"], xn)                                     # :308-311

@@ -280,3 +280,55 @@ def test_random_blocks_are_deterministic_and_distributed(hip, oracle, qt):
     v = h.download(np.float16, 100001).astype(np.float64)
     assert abs(v.mean()) < 0.02 and 0.97 < v.std() < 1.03
     assert np.all(f.download(np.float32, 1000) == 1.5)
+
+
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("pos", [-1, 256, 1 << 20])
+def test_decode_attention_outside_the_cache_is_zero(hip, pos, rope):
+    """A position outside [0, max_ctx) (a replayed graph past the cache end) reads and
+    writes no cache row and leaves a defined zero output rather than 0 / 0."""
+    n_heads, n_kv, hd, max_ctx = 8, 4, 128, 256
+    rng = np.random.default_rng(5)
+    qkv = rng.standard_normal((n_heads + 2 * n_kv) * hd).astype(np.float32)
+    kc = rng.standard_normal((n_kv, max_ctx, hd)).astype(np.float16)
+    vc = rng.standard_normal((n_kv, max_ctx, hd)).astype(np.float16)
+    dqkv, dkc, dvc = DeviceBuffer.from_numpy(qkv), DeviceBuffer.from_numpy(kc), DeviceBuffer.from_numpy(vc)
+    dpos = DeviceBuffer.from_numpy(np.array([pos], np.int32))
+    dws = DeviceBuffer(hip.asmhip_attention_decode_workspace(n_heads, hd, max_ctx) * 4)
+    dout = DeviceBuffer.from_numpy(np.full(n_heads * hd, 7.0, np.float32))
+    fn = hip.asmhip_attention_decode_rope if rope else hip.asmhip_attention_decode
+    args = (dqkv.ptr, dkc.ptr, dvc.ptr, dws.ptr, dout.ptr, n_heads, n_kv, hd, dpos.ptr, max_ctx)
+    _ok(hip, fn(*args, 10000.0, None) if rope else fn(*args, None))
+    synchronize()
+    assert np.all(dout.download(np.float32, n_heads * hd) == 0.0)
+    np.testing.assert_array_equal(dkc.download(np.float16, kc.shape), kc)
+    np.testing.assert_array_equal(dvc.download(np.float16, vc.shape), vc)
+    np.testing.assert_array_equal(dqkv.download(np.float32, qkv.size), qkv)
+
+
+@pytest.mark.parametrize("n", [5, 1024, 32769])
+@pytest.mark.parametrize("case", ["all-nan", "one-nan", "two-nan", "all-neg-inf", "neg-inf-and-one", "two-pos-inf"])
+def test_argmax_non_finite_as_numpy(hip, n, case):
+    """numpy.argmax semantics on non-finite logits: a NaN ranks first (the first NaN
+    wins), and an all -inf vector gives index 0 rather than no index at all."""
+    rng = np.random.default_rng(n)
+    logits = rng.standard_normal(n).astype(np.float32)
+    a, b = sorted(rng.choice(n, 2, replace=False))
+    if case == "all-nan":
+        logits[:] = np.nan
+    elif case == "one-nan":
+        logits[b] = np.nan
+    elif case == "two-nan":
+        logits[[a, b]] = np.nan
+    elif case == "all-neg-inf":
+        logits[:] = -np.inf
+    elif case == "neg-inf-and-one":
+        logits[:] = -np.inf
+        logits[b] = -1e30
+    else:
+        logits[[a, b]] = np.inf
+    dl = DeviceBuffer.from_numpy(logits)
+    dtok = DeviceBuffer.from_numpy(np.array([-1], np.int32))
+    _ok(hip, hip.asmhip_argmax(dl.ptr, n, dtok.ptr, None, None))
+    synchronize()
+    assert int(dtok.download(np.int32, 1)[0]) == int(np.argmax(logits))

@@ -50,6 +50,7 @@ def q4_kernel(hip):
 
 
 Q4_KERNELS = [native.Q4_KERNEL_FP32, native.Q4_KERNEL_MFMA]
+Q4_KERNEL_IDS = ["fp32", "mfma"]
 
 
 def _host_call(fn, *arrays_and_ints):
@@ -319,9 +320,10 @@ def test_bad_arguments_are_rejected(hip):
 
 # ---- both Q4_0 GGUF kernels, selected explicitly ------------------------------------------
 
-@pytest.mark.parametrize("kernel", Q4_KERNELS, ids=["fp32", "mfma"])
+@pytest.mark.parametrize("kernel", Q4_KERNELS, ids=Q4_KERNEL_IDS)
 @pytest.mark.parametrize("M,K", [s[1:] for s in CONFIG_SHAPES if s[0] == "q4"] +
-                         [(16, 256), (40, 16384), (12288, 4096), (22016, 4096), (32000, 4096), (300, 2304)])
+                         [(16, 256), (40, 16384), (12288, 4096), (22016, 4096), (32000, 4096), (300, 2304),
+                          (1, 4096), (255, 4096), (257, 4096), (5000, 4096)])
 def test_q4_kernels_at_config_shapes(hip, oracle, q4_kernel, kernel, M, K):
     q4_kernel(kernel)
     blocks, x = _weights(3 * M + K, M, K)
@@ -330,7 +332,7 @@ def test_q4_kernels_at_config_shapes(hip, oracle, q4_kernel, kernel, M, K):
     print(f"kernel {kernel} {M}x{K}: max err / row L1 = {worst:.2e}")
 
 
-@pytest.mark.parametrize("kernel", Q4_KERNELS, ids=["fp32", "mfma"])
+@pytest.mark.parametrize("kernel", Q4_KERNELS, ids=Q4_KERNEL_IDS)
 def test_q4_kernels_edge_cases(hip, oracle, q4_kernel, kernel):
     q4_kernel(kernel)
     test_all_eight_nibbles_give_zero(hip)
@@ -340,11 +342,12 @@ def test_q4_kernels_edge_cases(hip, oracle, q4_kernel, kernel):
         test_one_hot_x_picks_column_exactly(hip, oracle, "q4", col)
 
 
-def test_mfma_kernel_wide_dynamic_range_of_x(hip, oracle, q4_kernel):
+@pytest.mark.parametrize("kernel", [native.Q4_KERNEL_MFMA], ids=["mfma"])
+def test_mfma_kernel_wide_dynamic_range_of_x(hip, oracle, q4_kernel, kernel):
     """x spanning up to 2^40 inside a block, with zero weights placed on the
     largest entries of some rows: the two-level fixed point keeps every row
     within the bar."""
-    q4_kernel(native.Q4_KERNEL_MFMA)
+    q4_kernel(kernel)
     rng = np.random.default_rng(90)
     M, K = 256, 4096
     blocks, _ = _weights(91, M, K)
@@ -358,6 +361,28 @@ def test_mfma_kernel_wide_dynamic_range_of_x(hip, oracle, q4_kernel):
     y = _gguf_matvec(hip, "q4", blocks, x)
     worst = assert_matvec_close(y, oracle.matmul_q4_0_gguf(blocks, x, NT), oracle.dequantize_q4_0(blocks), x)
     assert worst < 1e-6
+
+
+@pytest.mark.parametrize("qt", ["q4", "q8"])
+@pytest.mark.parametrize("kernel", Q4_KERNELS, ids=Q4_KERNEL_IDS)
+@pytest.mark.parametrize("bad", ["nan", "inf", "-inf"])
+def test_non_finite_x_propagates(hip, oracle, q4_kernel, qt, kernel, bad):
+    """A NaN or infinite activation makes every row it touches non-finite, as
+    in the reference's fp32 arithmetic: no kernel may turn it into a finite
+    number (the matrix-core kernels prepare x as fixed point and carry a NaN
+    scale for such a block)."""
+    q4_kernel(kernel)
+    M, K = 300, 4096
+    blocks, x = _weights(44, M, K, qt)
+    x[1234] = {"nan": np.nan, "inf": np.inf, "-inf": -np.inf}[bad]
+    y = _gguf_matvec(hip, qt, blocks, x)
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = oracle.matmul_q4_0_gguf(blocks, x) if qt == "q4" else oracle.matmul_q8_0_gguf(blocks, x)
+    assert np.all(~np.isfinite(ref))  # the weight column at 1234 has no zero row here or NaN follows anyway
+    np.testing.assert_array_equal(~np.isfinite(y), ~np.isfinite(ref))
+    # the other blocks still count: a finite x with the same bytes stays finite
+    x[1234] = 0.5
+    assert np.all(np.isfinite(_gguf_matvec(hip, qt, blocks, x)))
 
 
 def test_forcing_mfma_on_an_ineligible_shape_is_an_error(hip, q4_kernel):
@@ -384,12 +409,13 @@ def _fused(hip, qtype, blocks, x, pre, arg, eps, y0):
 
 
 @pytest.mark.parametrize("qt,kernel", [("q4", native.Q4_KERNEL_FP32), ("q4", native.Q4_KERNEL_MFMA),
-                                       ("q8", native.Q4_KERNEL_AUTO)], ids=["q4-fp32", "q4-mfma", "q8"])
+                                       ("q8", native.Q4_KERNEL_AUTO), ("q8", native.Q4_KERNEL_FP32)],
+                         ids=["q4-fp32", "q4-mfma", "q8", "q8-fp32"])
 @pytest.mark.parametrize("pre", ["none", "rmsnorm", "swiglu"])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_fused_matvec(hip, oracle, q4_kernel, qt, kernel, pre, accumulate):
-    q4_kernel(kernel)
     M, K = 1000, 4096 if pre != "swiglu" else 11008
+    q4_kernel(kernel)
     blocks, x = _weights(17 + K, M, K, qt)
     rng = np.random.default_rng(5)
     arg = None
@@ -474,7 +500,8 @@ def test_matmul_swiglu(hip, oracle, q4_kernel, qt, kernel, H, K, pre):
     assert np.all(np.abs(h.astype(np.float64) - h_ref) <= bound)
 
 
-@pytest.mark.parametrize("H,K", [(8, 256), (24, 4096), (1000, 768), (2048, 2560), (4096, 8192), (136, 96)])
+@pytest.mark.parametrize("H,K", [(8, 256), (24, 4096), (1000, 768), (2048, 2560), (4096, 8192), (136, 96),
+                                 (8, 4096), (2056, 4096), (11008, 4096)])
 def test_matmul_swiglu_shapes(hip, H, K):
     """Bitwise the two-step result (matvec of the same rows, then asmhip_silu_hadamard)
     at shapes from one tile to several tiles per workgroup, MFMA stream and not."""

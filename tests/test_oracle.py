@@ -421,3 +421,88 @@ def test_q5_gguf_equals_split_path(oracle):
     w = ops_ref.dequantize_q5_0(ql, qh, sc)
     np.testing.assert_array_equal(oracle.dequantize_q5_0(blocks), w)
     np.testing.assert_array_equal(gguf.dequantize_q5_0(blocks), w)
+
+
+# ---- SiLU . up (swiglu_avx2.asm:45-81) against the mathematics ----------------------------
+
+_ULP = 2.0 ** -23
+
+
+def _silu_pins(fn) -> list[str]:
+    """Every check of silu(g) * u that the mathematics fixes, run on `fn(gate, up)`;
+    returns the names of the checks that fail (empty: pinned)."""
+    failed = []
+    f32 = np.float32
+    # silu(0) = 0 exactly, whatever u is
+    u = np.array([1.0, -3.5, 7.25, 1e30], f32)
+    if not np.all(fn(np.zeros(4, f32), u) == 0.0):
+        failed.append("silu(0) = 0")
+    # g = ln 3: 1 + e^-g = 4/3, so silu(g) u = 0.75 g u (to the rounding of the fp32 steps)
+    g = np.full(3, np.log(3.0), f32)
+    u = np.array([1.0, 2.0, -0.5], f32)
+    want = 0.75 * g.astype(np.float64) * u
+    if not np.all(np.abs(fn(g, u) - want) <= 4 * _ULP * np.abs(want)):
+        failed.append("silu(ln 3) = 0.75 ln 3")
+    # silu(g) - silu(-g) = g sigma(g) + g sigma(-g) = g, over a sweep of g (u = 1)
+    gs = np.concatenate([np.linspace(-30, 30, 4001), np.geomspace(1e-6, 1e3, 200)]).astype(f32)
+    ones = np.ones_like(gs)
+    pos, neg = fn(gs, ones).astype(np.float64), fn(-gs, ones).astype(np.float64)
+    if not np.all(np.abs((pos - neg) - gs) <= 4 * _ULP * (np.abs(pos) + np.abs(neg)) + 1e-45):
+        failed.append("silu(g) - silu(-g) = g")
+    # large |g|: e^-g vanishes next to 1, so silu(g) u = g u exactly; the negative side is
+    # g e^g to fp32 rounding, and past the fp32 range of 1 + e^-g (g < -88.7) the rounded
+    # denominator is infinite and the result a signed zero, as in the reference's fstp dword
+    big = np.array([20.0, 50.0, 88.0, 1e4], f32)
+    u = np.array([1.5, -2.0, 0.25, 3.0], f32)
+    if not np.array_equal(fn(big, u), big * u):
+        failed.append("silu(g) = g for large g")
+    gneg = np.array([-20.0, -50.0, -80.0], f32)
+    want = gneg.astype(np.float64) / (1.0 + np.exp(-gneg.astype(np.float64)))
+    if not np.all(np.abs(fn(gneg, np.ones(3, f32)) - want) <= 4 * _ULP * np.abs(want)):
+        failed.append("silu(g) = g e^g for large -g")
+    if not np.all(fn(np.array([-100.0, -1e4], f32), np.array([2.0, 1.0], f32)) == 0.0):
+        failed.append("silu(g) = 0 where 1 + e^-g overflows fp32")
+    # a float64 closed form over random g, u (three fp32 roundings: 1 + e^-g, /, *)
+    rng = np.random.default_rng(11)
+    g = (rng.standard_normal(20000) * 6).astype(f32)
+    u = rng.standard_normal(20000).astype(f32)
+    g64 = g.astype(np.float64)
+    want = g64 / (1.0 + np.exp(-g64)) * u
+    if not np.all(np.abs(fn(g, u) - want) <= 4 * _ULP * np.abs(want) + 1e-44):
+        failed.append("float64 closed form")
+    return failed
+
+
+def test_silu_hadamard_pinned_by_the_mathematics(oracle):
+    assert _silu_pins(oracle.silu_hadamard) == []
+
+
+def test_silu_hadamard_agrees_with_the_python_reference_formula(oracle):
+    """generate.py:370's numpy form (ops_ref.silu_hadamard) in fp32, within the rounding of
+    the two fp32 evaluations of exp."""
+    rng = np.random.default_rng(12)
+    g = (rng.standard_normal(5000) * 8).astype(np.float32)
+    u = rng.standard_normal(5000).astype(np.float32)
+    with np.errstate(over="ignore"):
+        ref = ops_ref.silu_hadamard(g, u).astype(np.float64)
+    got = oracle.silu_hadamard(g, u).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 8 * _ULP * np.abs(ref) + 1e-44)
+
+
+@pytest.mark.parametrize("mistake", ["exp(+g)", "g * (1 + exp(-g))", "sigmoid only", "up ignored"])
+def test_silu_pins_catch_plausible_mistakes(mistake):
+    """The checks above reject each plausible slip, so passing them means something."""
+    def mutant(gate, up):
+        g = gate.astype(np.float64)
+        if mistake == "exp(+g)":
+            r = g / (1.0 + np.exp(g))
+        elif mistake == "g * (1 + exp(-g))":
+            r = g * (1.0 + np.exp(-g))
+        elif mistake == "sigmoid only":
+            r = 1.0 / (1.0 + np.exp(-g))
+        else:
+            return (g / (1.0 + np.exp(-g))).astype(np.float32)
+        return (r * up).astype(np.float32)
+
+    with np.errstate(over="ignore", invalid="ignore"):
+        assert _silu_pins(mutant) != []
