@@ -609,6 +609,60 @@ extern "C" int asmhip_attention_decode_rope(const float* qkv, void* k_cache, voi
                               true, theta, (hipStream_t)stream);
 }
 
+// ---- decode attention without a caller workspace -----------------------------------------
+//
+// For callers that cannot allocate (graph capture, tight serving loops): the
+// split partials live in `scratch`, a fixed array in every device's copy of the
+// library, instead of a workspace argument.  Its device address differs per GPU
+// and is only known through hipGetSymbolAddress (host code must never pass the
+// array's own name to a kernel), so it is looked up once per device, with that
+// device current, on the first call there.  The split kernel writes every
+// split's partial (empty splits included) before the merge reads them, so
+// nothing needs clearing between calls; calls that overlap on one GPU share the
+// array and race.
+namespace {
+constexpr int64_t kNoAllocScratchFloats = 1 << 20;  // 4 MiB: n_heads * ceil(max_ctx / 128) * (head_dim + 2)
+__device__ __align__(256) float scratch[kNoAllocScratchFloats];
+float* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(float** out) {
+    int dev = 0;
+    const int rc = current_device(&dev);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        ASMHIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(kHipError, "hipGetSymbolAddress returned no address for the attention scratch");
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return kOk;
+}
+}  // namespace
+
+extern "C" int64_t asmhip_attention_decode_noalloc_max_floats(void) { return kNoAllocScratchFloats; }
+
+extern "C" int asmhip_attention_decode_rope_noalloc(const float* qkv, void* k_cache, void* v_cache, float* out,
+                                                    int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
+                                                    int max_ctx, float theta, void* stream) {
+    if (!qkv || !k_cache || !v_cache || !out || !pos_dev) return fail(kInvalidArgument, "null pointer argument");
+    if (n_heads <= 0 || head_dim <= 0 || max_ctx <= 0 || head_dim % 2)
+        return fail(kInvalidArgument, "bad attention shape");
+    const int64_t need = attn_decode_workspace(n_heads, head_dim, max_ctx);
+    if (need > kNoAllocScratchFloats)
+        return fail(kInvalidArgument,
+                    "attention without a workspace: n_heads %d x %d splits x (head_dim %d + 2) = %lld floats "
+                    "exceeds the %lld-float scratch; pass a workspace to asmhip_attention_decode_rope",
+                    n_heads, attn_decode_splits(max_ctx), head_dim, (long long)need,
+                    (long long)kNoAllocScratchFloats);
+    float* part = nullptr;
+    const int rc = scratch_for_current_device(&part);
+    if (rc) return rc;
+    return attn_decode_launch(qkv, k_cache, v_cache, part, out, n_heads, n_kv_heads, head_dim, pos_dev, max_ctx,
+                              true, theta, (hipStream_t)stream);
+}
+
 extern "C" int asmhip_embed_q4_0(const void* table, const int* token_dev, float* x, int n_vocab, int dim,
                                  void* stream) {
     if (!table || !token_dev || !x) return fail(kInvalidArgument, "null pointer argument");

@@ -227,6 +227,19 @@ ASMHIP_API int asmhip_attention_decode(const float* q, const void* k_cache, cons
 ASMHIP_API int asmhip_attention_decode_rope(const float* qkv, void* k_cache, void* v_cache, float* workspace,
                                             float* out, int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
                                             int max_ctx, float theta, void* stream);
+/* asmhip_attention_decode_rope without the workspace argument.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory (HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * split partials go to a fixed per-device scratch array of
+ * asmhip_attention_decode_noalloc_max_floats() floats (4 MiB); shapes needing
+ * more (n_heads * ceil(max_ctx / 128) * (head_dim + 2) floats) are rejected with
+ * ASMHIP_ERR_INVALID_ARGUMENT.  Calls that overlap on one GPU share the array and
+ * race; nothing in it needs clearing between calls.  Same results, bit for bit,
+ * as asmhip_attention_decode_rope. */
+ASMHIP_API int64_t asmhip_attention_decode_noalloc_max_floats(void);
+ASMHIP_API int asmhip_attention_decode_rope_noalloc(const float* qkv, void* k_cache, void* v_cache, float* out,
+                                                    int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
+                                                    int max_ctx, float theta, void* stream);
 /* x = row *token_dev of a Q4_0 embedding table [n_vocab][dim]
  * (generate.py:262, the table dequantized by get_tensor :169-182). */
 ASMHIP_API int asmhip_embed_q4_0(const void* table, const int* token_dev, float* x, int n_vocab, int dim,
