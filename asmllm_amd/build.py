@@ -26,6 +26,7 @@ LIB_PATH = LIB_DIR / "libasmllm.so"
 SOURCES = [
     "matvec.hip",
     "matvec_mfma.hip",
+    "measure.hip",
     "decode_ops.hip",
     "quant.hip",
     "gemm.hip",

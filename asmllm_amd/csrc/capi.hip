@@ -641,6 +641,10 @@ int scratch_for_current_device(float** out) {
 }
 }  // namespace
 
+extern "C" int asmhip_stream_read(const void* buf, int64_t bytes, void* sink, void* stream) {
+    return stream_read_launch(buf, bytes, static_cast<uint32_t*>(sink), (hipStream_t)stream);
+}
+
 extern "C" int64_t asmhip_attention_decode_noalloc_max_floats(void) { return kNoAllocScratchFloats; }
 
 extern "C" int asmhip_attention_decode_rope_noalloc(const float* qkv, void* k_cache, void* v_cache, float* out,

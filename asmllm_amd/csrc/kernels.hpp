@@ -76,6 +76,10 @@ int split_mfma_launch(int bits, const void* qs, const uint8_t* qh, const float* 
 // scaled by both fp16 scales and accumulated in block order.
 int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t M, int64_t K, hipStream_t stream);
 
+// Plain streaming read of `bytes` in one launch (measurement: the single-launch
+// read floor); `sink` is 4 KB of device memory the kernel practically never writes.
+int stream_read_launch(const void* buf, int64_t bytes, uint32_t* sink, hipStream_t st);
+
 // Exact fp32 dequantization of GGUF blocks, row-major [rows][K].
 int dequant_launch(QuantType qt, const void* w, float* out, int64_t rows, int64_t K, hipStream_t stream);
 

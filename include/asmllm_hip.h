@@ -227,6 +227,12 @@ ASMHIP_API int asmhip_attention_decode(const float* q, const void* k_cache, cons
 ASMHIP_API int asmhip_attention_decode_rope(const float* qkv, void* k_cache, void* v_cache, float* workspace,
                                             float* out, int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
                                             int max_ctx, float theta, void* stream);
+/* Measurement, not part of the path: reads `bytes` (< 2 GiB) of device memory
+ * in one launch, every workgroup one contiguous chunk with all loads issued up
+ * front, and keeps nothing; `sink` is 4 KB of device memory.  Its time is the
+ * single-launch read floor a matvec over the same bytes can approach (no
+ * counterpart in the reference). */
+ASMHIP_API int asmhip_stream_read(const void* buf, int64_t bytes, void* sink, void* stream);
 /* asmhip_attention_decode_rope without the workspace argument.  No counterpart
  * in the reference: it is for callers that cannot allocate device memory (HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
