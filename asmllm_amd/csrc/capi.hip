@@ -609,6 +609,21 @@ extern "C" int asmhip_attention_decode_rope(const float* qkv, void* k_cache, voi
                               true, theta, (hipStream_t)stream);
 }
 
+extern "C" int asmhip_rope_table(float* table, int head_dim, int max_ctx, float theta, void* stream) {
+    return rope_table_launch(table, head_dim, max_ctx, theta, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_attention_decode_rope_table(const float* qkv, void* k_cache, void* v_cache, float* workspace,
+                                                  float* out, int n_heads, int n_kv_heads, int head_dim,
+                                                  const int* pos_dev, int max_ctx, const float* rope_table,
+                                                  void* stream) {
+    if (!qkv || !k_cache || !v_cache || !workspace || !out || !pos_dev || !rope_table)
+        return fail(kInvalidArgument, "null pointer argument");
+    if (n_heads <= 0 || max_ctx <= 0 || head_dim % 2) return fail(kInvalidArgument, "bad attention shape");
+    return attn_decode_launch(qkv, k_cache, v_cache, workspace, out, n_heads, n_kv_heads, head_dim, pos_dev, max_ctx,
+                              true, 0.f, (hipStream_t)stream, rope_table);
+}
+
 // ---- decode attention without a caller workspace -----------------------------------------
 //
 // For callers that cannot allocate (graph capture, tight serving loops): the

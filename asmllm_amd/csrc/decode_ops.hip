@@ -70,10 +70,14 @@ __device__ __forceinline__ void rope_angle(int p, int hd, int pos, float theta, 
     *s = (float)sin(ang);
 }
 
+// Two products and a sum, each rounded (mulss, mulss, subss / addss in
+// rope_avx2.asm:114-145): contraction off, or the compiler fuses one product
+// into an fma, and which one depends on the code around the call.
 __device__ __forceinline__ void rotate(float* v, float c, float s) {
+#pragma clang fp contract(off)
     const float a = v[0], b = v[1];
-    v[0] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-    v[1] = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+    v[0] = a * c - b * s;
+    v[1] = a * s + b * c;
 }
 
 __global__ __launch_bounds__(kBlock) void rope_kernel(float* __restrict__ q, float* __restrict__ k, int n_q_heads,
@@ -205,11 +209,14 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(const float* __restri
 // [m, l, acc[HD]] to `part`, and attn_decode_merge combines the S partials of a
 // head in split order into out = acc / l.
 //
-// ROPE = true also does what rope_kv_write does, inside the same launch: q and
-// the new k are rotated at `pos` (angles as rope_angle), the new k and v are
-// rounded to fp16 and written to the caches at `pos` (by the workgroup of the
-// first query head of the kv group), and the workgroup whose split holds `pos`
-// uses those fp16 values instead of reading the row it writes.
+// ROPE != kRopeNone also does what rope_kv_write does, inside the same launch:
+// q and the new k are rotated at `pos`, the new k and v are rounded to fp16 and
+// written to the caches at `pos` (by the workgroup of the first query head of
+// the kv group), and the workgroup whose split holds `pos` uses those fp16
+// values instead of reading the row it writes.  kRopeTheta forms the angles
+// (rope_angle, double precision: about 600 fp64 instructions that every wave
+// waits for); kRopeTable reads the same cos/sin values from a table that
+// rope_table_kernel filled once, a load that travels with the k/v loads.
 // Sum over aligned groups of N lanes (N = 8 or 16), every lane receiving its
 // group's sum, with DPP adds instead of LDS permutes: quad_perm [1,0,3,2] and
 // [2,3,0,1] sum the quads, row_half_mirror pairs quad 0 with 1 (2 with 3),
@@ -258,11 +265,13 @@ struct HalfRow {
 
 constexpr uint32_t kAttnPastEnd = 0xFFFFFF00u;  // buffer offset that loads zeros
 
-template <int HD, bool ROPE>
+enum RopeMode : int { kRopeNone = 0, kRopeTheta = 1, kRopeTable = 2 };
+
+template <int HD, int ROPE>
 __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __restrict__ qkv, __half* kc, __half* vc,
                                                              float* __restrict__ part, int n_heads, int n_kv,
                                                              const int* __restrict__ pos_ptr, int max_ctx,
-                                                             float theta) {
+                                                             float theta, const float* __restrict__ rope_table) {
     constexpr int E = HD % 64 == 0 ? 8 : 6;               // fp16 elements per lane
     constexpr int kLanes = HD / E;                        // lanes per position
     static_assert(HD == E * kLanes && kWave % kLanes == 0, "head_dim 48, 64 or 128");
@@ -293,6 +302,16 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
         const float2 a = *reinterpret_cast<const float2*>(qkv + (size_t)h * HD + E * c + t);
         qv[t] = a.x, qv[t + 1] = a.y;
     }
+    // cos, sin of this lane's E / 2 pairs (pair E/2 c + i at 2i, 2i + 1)
+    float csl[E];
+    if constexpr (ROPE == kRopeTable) {
+        const float* row = rope_table + (size_t)(n_pos > 0 ? pos : 0) * HD + E * c;
+#pragma unroll
+        for (int t = 0; t < E; t += 2) {
+            const float2 a = *reinterpret_cast<const float2*>(row + t);
+            csl[t] = a.x, csl[t + 1] = a.y;
+        }
+    }
     HalfRow<E> kr[kRows], vr[kRows];
     const uint32_t cache_bytes = (uint32_t)n_kv * (uint32_t)max_ctx * (uint32_t)(2 * HD);  // < 4 GB, checked at launch
     const auto kres = make_rsrc(kc, cache_bytes), vres = make_rsrc(vc, cache_bytes);
@@ -300,7 +319,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         const int p = p0 + r * kRowPos + w * kGroups + g;
-        const bool live = p < p1 && !(ROPE && p == pos);
+        const bool live = p < p1 && !(ROPE != kRopeNone && p == pos);
         off[r] = live ? 2u * (uint32_t)(head_off + (size_t)p * HD) : kAttnPastEnd;
         if constexpr (E == 8) {
             const uint4 a = buf_load_b128(kres, off[r]);
@@ -318,13 +337,17 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
             vr[r] = off[r] != kAttnPastEnd ? HalfRow<E>::load(vc + off[r] / 2) : HalfRow<E>::zero();
         }
     }
-    if constexpr (ROPE) {
+    if constexpr (ROPE == kRopeTheta) {
         if (threadIdx.x < HD / 2 && n_pos > 0)
             rope_angle(threadIdx.x, HD, pos, theta, &cs[2 * threadIdx.x], &cs[2 * threadIdx.x + 1]);
         __syncthreads();
+#pragma unroll
+        for (int t = 0; t < E; ++t) csl[t] = cs[E * c + t];
+    }
+    if constexpr (ROPE != kRopeNone) {
         if (n_pos > 0) {
 #pragma unroll
-            for (int i = 0; i < E / 2; ++i) rotate(&qv[2 * i], cs[2 * (E / 2 * c + i)], cs[2 * (E / 2 * c + i) + 1]);
+            for (int i = 0; i < E / 2; ++i) rotate(&qv[2 * i], csl[2 * i], csl[2 * i + 1]);
         }
         if (p0 <= pos && pos < p1) {
             // the new row: rotated k and v of kv head kvh, rounded to fp16
@@ -334,7 +357,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
 #pragma unroll
             for (int i = 0; i < E / 2; ++i) {
                 float kk[2] = {kn[2 * i], kn[2 * i + 1]};
-                rotate(kk, cs[2 * (E / 2 * c + i)], cs[2 * (E / 2 * c + i) + 1]);
+                rotate(kk, csl[2 * i], csl[2 * i + 1]);
                 kq.w[i] = (uint32_t)__half_as_ushort(__float2half_rn(kk[0])) |
                           ((uint32_t)__half_as_ushort(__float2half_rn(kk[1])) << 16);
                 vq.w[i] = (uint32_t)__half_as_ushort(__float2half_rn(vn[2 * i])) |
@@ -597,8 +620,27 @@ int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx) {
     return (int64_t)n_heads * attn_decode_splits(max_ctx) * (hd + 2);
 }
 
+namespace {
+template <int HD>
+void launch_attn_decode(int mode, dim3 grid, hipStream_t st, const float* qkv, __half* kc, __half* vc, float* part,
+                        float* out, int n_heads, int n_kv, const int* pos_ptr, int max_ctx, float theta,
+                        const float* rope_table) {
+    if (mode == kRopeTable)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeTable>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                           n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
+    else if (mode == kRopeTheta)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeTheta>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                           n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
+    else
+        hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeNone>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                           n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
+    hipLaunchKernelGGL((attn_decode_merge<HD>), dim3(n_heads), dim3(HD), 0, st, part, out, (int)grid.y);
+}
+}  // namespace
+
 int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* part, float* out, int n_heads,
-                       int n_kv, int hd, const int* pos_ptr, int max_ctx, bool rope, float theta, hipStream_t st) {
+                       int n_kv, int hd, const int* pos_ptr, int max_ctx, bool rope, float theta, hipStream_t st,
+                       const float* rope_table) {
     if (n_kv <= 0 || n_heads % n_kv) return fail(kInvalidArgument, "attention: n_heads %% n_kv_heads != 0");
     if (max_ctx <= 0) return fail(kInvalidArgument, "attention: max_ctx must be > 0");
     const int splits = attn_decode_splits(max_ctx);
@@ -606,38 +648,45 @@ int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* pa
         return fail(kUnsupported, "attention: max_ctx %d exceeds %d positions", max_ctx, 64 * kAttnSplitLen);
     if ((uintptr_t)qkv % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
         return fail(kInvalidArgument, "attention: q and the caches must be 16-byte aligned");
+    if (rope_table && (uintptr_t)rope_table % 8)
+        return fail(kInvalidArgument, "attention: the RoPE table must be 8-byte aligned");
     if ((int64_t)n_kv * max_ctx * hd * 2 >= (int64_t)kAttnPastEnd)
         return fail(kUnsupported, "attention: caches of 4 GB or more per layer are not supported");
+    const int mode = !rope ? kRopeNone : rope_table ? kRopeTable : kRopeTheta;
     const dim3 grid(n_heads, splits);
     __half* kc = (__half*)k_cache;
     __half* vc = (__half*)v_cache;
-    if (hd == 128) {
-        if (rope)
-            hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
-                               n_heads, n_kv, pos_ptr, max_ctx, theta);
-        else
-            hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
-                               n_heads, n_kv, pos_ptr, max_ctx, theta);
-        hipLaunchKernelGGL((attn_decode_merge<128>), dim3(n_heads), dim3(128), 0, st, part, out, splits);
-    } else if (hd == 64) {
-        if (rope)
-            hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
-                               n_heads, n_kv, pos_ptr, max_ctx, theta);
-        else
-            hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
-                               n_heads, n_kv, pos_ptr, max_ctx, theta);
-        hipLaunchKernelGGL((attn_decode_merge<64>), dim3(n_heads), dim3(64), 0, st, part, out, splits);
-    } else if (hd == 48) {
-        if (rope)
-            hipLaunchKernelGGL((attn_decode_kernel<48, true>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
-                               n_heads, n_kv, pos_ptr, max_ctx, theta);
-        else
-            hipLaunchKernelGGL((attn_decode_kernel<48, false>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
-                               n_heads, n_kv, pos_ptr, max_ctx, theta);
-        hipLaunchKernelGGL((attn_decode_merge<48>), dim3(n_heads), dim3(48), 0, st, part, out, splits);
-    } else {
+    if (hd == 128)
+        launch_attn_decode<128>(mode, grid, st, qkv, kc, vc, part, out, n_heads, n_kv, pos_ptr, max_ctx, theta,
+                                rope_table);
+    else if (hd == 64)
+        launch_attn_decode<64>(mode, grid, st, qkv, kc, vc, part, out, n_heads, n_kv, pos_ptr, max_ctx, theta,
+                               rope_table);
+    else if (hd == 48)
+        launch_attn_decode<48>(mode, grid, st, qkv, kc, vc, part, out, n_heads, n_kv, pos_ptr, max_ctx, theta,
+                               rope_table);
+    else
         return fail(kUnsupported, "attention: head_dim %d (supported: 48, 64, 128)", hd);
-    }
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+// table[p][2i] = cos, table[p][2i + 1] = sin of pair i at position p (rope_angle).
+__global__ __launch_bounds__(kBlock) void rope_table_kernel(float* __restrict__ table, int hd, int max_ctx,
+                                                            float theta) {
+    const int half = hd >> 1;
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= (int64_t)max_ctx * half) return;
+    const int pair = (int)(i % half), p = (int)(i / half);
+    rope_angle(pair, hd, p, theta, &table[2 * i], &table[2 * i + 1]);
+}
+
+int rope_table_launch(float* table, int hd, int max_ctx, float theta, hipStream_t st) {
+    if (!table) return fail(kInvalidArgument, "rope table: null pointer");
+    if (hd <= 0 || hd % 2 || max_ctx <= 0) return fail(kInvalidArgument, "rope table: bad shape");
+    const int64_t n = (int64_t)max_ctx * (hd / 2);
+    hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, st, table,
+                       hd, max_ctx, theta);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

@@ -118,8 +118,13 @@ int attention_launch(const float* q, const float* k, const float* v, float* y, i
 constexpr int kAttnSplitLen = 128;
 int attn_decode_splits(int max_ctx);
 int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx);
+// rope_table (optional, with rope): [max_ctx][hd] floats from rope_table_launch,
+// read instead of forming the angles in the kernel.
 int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* part, float* out, int n_heads,
-                       int n_kv, int hd, const int* pos_ptr, int max_ctx, bool rope, float theta, hipStream_t st);
+                       int n_kv, int hd, const int* pos_ptr, int max_ctx, bool rope, float theta, hipStream_t st,
+                       const float* rope_table = nullptr);
+// table[p][2i], table[p][2i + 1] = cos, sin of RoPE pair i at position p < max_ctx.
+int rope_table_launch(float* table, int hd, int max_ctx, float theta, hipStream_t st);
 
 // x = row *token of a Q4_0 or Q8_0 GGUF table [n_vocab][dim], exact.
 int embed_launch(QuantType qt, const void* table, const int* token, float* x, int n_vocab, int dim, hipStream_t st);

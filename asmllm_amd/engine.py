@@ -20,7 +20,8 @@ stream, so it can be captured once into a HIP graph and replayed per token:
     the argmax kernel writes the next token and advances the position, so a
     replayed graph walks the sequence without host involvement;
   * RoPE and the KV-cache write are fused into the attention launch
-    (asmhip_attention_decode_rope);
+    (asmhip_attention_decode_rope_table), its cos/sin read from a table of
+    every position's angles formed once at set-up (asmhip_rope_table);
   * the KV cache is fp16, head-major [n_kv_heads][max_ctx][head_dim] per layer
     (the reference keeps fp32 [128][heads][head_dim], generate.py:252-253);
   * head_dim 48 (the reference's stories15M demo model, dim 288), 64 or 128;
@@ -186,6 +187,10 @@ class DecodeEngine:
         self.xn = None if self.fuse_norm else DeviceBuffer(4 * s.dim)
         ws = self.lib.asmhip_attention_decode_workspace(s.n_heads, s.head_dim, self.max_ctx)
         self.workspace = DeviceBuffer(4 * max(int(ws), 1))
+        # cos/sin of every RoPE angle, formed once instead of in every attention launch
+        self.rope_table = DeviceBuffer(4 * self.max_ctx * s.head_dim)
+        check(self.lib.asmhip_rope_table(self.rope_table.ptr, s.head_dim, self.max_ctx, ctypes.c_float(s.theta),
+                                         self.stream.handle), "rope table")
         self.token = DeviceBuffer(4)
         self.pos = DeviceBuffer(4)
         self.vocab: list[str] = []
@@ -333,9 +338,10 @@ class DecodeEngine:
         check(embed(self.embed.ptr, self.token.ptr, self.x.ptr, s.vocab, d, st), "embed")
         for ly in self.layers:
             normed(ly.attn_norm, s.qkv_rows, ly.wqkv, self.qkv.ptr, "qkv matvec")
-            check(L.asmhip_attention_decode_rope(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr, self.workspace.ptr,
-                                                 self.attn.ptr, s.n_heads, s.n_kv_heads, hd, self.pos.ptr,
-                                                 self.max_ctx, ctypes.c_float(s.theta), st), "rope + attention")
+            check(L.asmhip_attention_decode_rope_table(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr,
+                                                       self.workspace.ptr, self.attn.ptr, s.n_heads, s.n_kv_heads, hd,
+                                                       self.pos.ptr, self.max_ctx, self.rope_table.ptr, st),
+                  "rope + attention")
             mv(ly.wo, self.attn.ptr, self.x.ptr, d, d, NONE, None, 1, "o matvec")
             xin, pre, arg = norm_in(ly.ffn_norm)
             check(L.asmhip_matmul_swiglu(Q4, ly.wgu.ptr, xin, self.ffn.ptr, h, d, pre, arg, eps, self.gu.ptr, st),

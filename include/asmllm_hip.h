@@ -227,6 +227,18 @@ ASMHIP_API int asmhip_attention_decode(const float* q, const void* k_cache, cons
 ASMHIP_API int asmhip_attention_decode_rope(const float* qkv, void* k_cache, void* v_cache, float* workspace,
                                             float* out, int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
                                             int max_ctx, float theta, void* stream);
+/* The RoPE angles of generate.py:282-283 (rope_avx2.asm:52-146) for every
+ * position 0..max_ctx-1, formed once: table[p][2i] = cos and table[p][2i + 1]
+ * = sin of pair i (head_dim / 2 pairs) at position p, max_ctx * head_dim
+ * floats, the same values asmhip_rope_kv_write forms per call.
+ * asmhip_attention_decode_rope_table is asmhip_attention_decode_rope with the
+ * angles read from such a table (8-byte aligned) instead of formed in the
+ * launch: same results, bit for bit. */
+ASMHIP_API int asmhip_rope_table(float* table, int head_dim, int max_ctx, float theta, void* stream);
+ASMHIP_API int asmhip_attention_decode_rope_table(const float* qkv, void* k_cache, void* v_cache, float* workspace,
+                                                  float* out, int n_heads, int n_kv_heads, int head_dim,
+                                                  const int* pos_dev, int max_ctx, const float* rope_table,
+                                                  void* stream);
 /* Measurement, not part of the path: reads `bytes` (< 2 GiB) of device memory
  * in one launch, every workgroup one contiguous chunk with all loads issued up
  * front, and keeps nothing; `sink` is 4 KB of device memory.  Its time is the

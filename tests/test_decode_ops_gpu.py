@@ -155,6 +155,12 @@ def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos,
     fout = DeviceBuffer(n_heads * hd * 4)
     _ok(hip, hip.asmhip_attention_decode_rope(fqkv.ptr, fkc.ptr, fvc.ptr, dws.ptr, fout.ptr, n_heads, n_kv, hd,
                                               dpos.ptr, max_ctx, 10000.0, None))
+    # and with the angles from a table formed once
+    tqkv, tkc, tvc = DeviceBuffer.from_numpy(qkv), DeviceBuffer.from_numpy(kc), DeviceBuffer.from_numpy(vc)
+    tout, table = DeviceBuffer(n_heads * hd * 4), DeviceBuffer(max_ctx * hd * 4)
+    _ok(hip, hip.asmhip_rope_table(table.ptr, hd, max_ctx, 10000.0, None))
+    _ok(hip, hip.asmhip_attention_decode_rope_table(tqkv.ptr, tkc.ptr, tvc.ptr, dws.ptr, tout.ptr, n_heads, n_kv,
+                                                    hd, dpos.ptr, max_ctx, table.ptr, None))
     _ok(hip, hip.asmhip_rope_kv_write(dqkv.ptr, dkc.ptr, dvc.ptr, n_heads, n_kv, hd, dpos.ptr, max_ctx, 10000.0,
                                       None))
     _ok(hip, hip.asmhip_attention_decode(dqkv.ptr, dkc.ptr, dvc.ptr, dws.ptr, dout.ptr, n_heads, n_kv, hd,
@@ -187,6 +193,26 @@ def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos,
     np.testing.assert_array_equal(fkc.download(np.float16, (n_kv, max_ctx, hd)), got_kc)
     np.testing.assert_array_equal(fvc.download(np.float16, (n_kv, max_ctx, hd)), got_vc)
     np.testing.assert_array_equal(fqkv.download(np.float32, qkv.size), qkv)  # q left unrotated
+    np.testing.assert_array_equal(tout.download(np.float32, (n_heads, hd)), out)
+    np.testing.assert_array_equal(tkc.download(np.float16, (n_kv, max_ctx, hd)), got_kc)
+    np.testing.assert_array_equal(tvc.download(np.float16, (n_kv, max_ctx, hd)), got_vc)
+    np.testing.assert_array_equal(tqkv.download(np.float32, qkv.size), qkv)
+
+
+@pytest.mark.parametrize("hd,max_ctx,theta", [(128, 2176, 10000.0), (64, 300, 500000.0), (48, 8192, 10000.0)])
+def test_rope_table_angles(hip, hd, max_ctx, theta):
+    """table[p][2i], [2i + 1] = cos, sin of p * theta^(-2i / hd): the exponent a
+    float32 quotient (divss in rope_avx2.asm), the angle and its cos / sin in
+    float64, rounded to float32 (to within an ulp of numpy's float64 math)."""
+    table = DeviceBuffer(max_ctx * hd * 4)
+    _ok(hip, hip.asmhip_rope_table(table.ptr, hd, max_ctx, theta, None))
+    synchronize()
+    got = table.download(np.float32, (max_ctx, hd // 2, 2))
+    e = (np.float32(-2) * np.arange(hd // 2, dtype=np.float32)) / np.float32(hd)
+    ang = np.power(np.float64(np.float32(theta)), e.astype(np.float64))[None, :] * np.arange(max_ctx)[:, None]
+    np.testing.assert_allclose(got[..., 0], np.cos(ang).astype(np.float32), rtol=0, atol=2e-7)
+    np.testing.assert_allclose(got[..., 1], np.sin(ang).astype(np.float32), rtol=0, atol=2e-7)
+    assert np.array_equal(got[0, :, 0], np.ones(hd // 2, np.float32)) and not got[0, :, 1].any()
 
 
 
