@@ -629,6 +629,59 @@ TRAFFIC_PASSES = (
 )
 
 
+def _pmc_passes(passes, workload: list[str], kinds: dict, timeout_s: int = 150) -> dict | None:
+    """Runs `bench.py <workload>` once per counter pass under rocprofv3 --pmc (a
+    child process each) and returns, per kernel kind, the mean of every counter
+    over that kind's dispatches and the mean dispatch duration in microseconds
+    (`kinds` maps a kind to a predicate on the kernel name).  None when
+    rocprofv3 is unavailable or a pass fails."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        log("rocprofv3 not found: counters not collected")
+        return None
+    vals: dict[str, dict[str, float]] = {k: {} for k in kinds}
+    durs: dict[str, list[float]] = {k: [] for k in kinds}
+    env = dict(os.environ, TMPDIR="/tmp")
+    with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+        for n, counters in enumerate(passes):
+            cmd = [exe, "--pmc", *counters, "--output-format", "csv", "-d", tmp, "-o", f"pass{n}", "--",
+                   sys.executable, str(ROOT / "bench.py"), *workload]
+            try:
+                subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, check=True,
+                               stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+            except (subprocess.SubprocessError, OSError) as e:
+                log(f"rocprofv3 pass {n} failed ({e}): counters not collected")
+                return None
+            files = list(Path(tmp).rglob(f"pass{n}_counter_collection.csv"))
+            if not files:
+                log(f"rocprofv3 pass {n} wrote no counter file: counters not collected")
+                return None
+            acc: dict[str, dict[str, list[float]]] = {k: {} for k in kinds}
+            seen: set = set()
+            with open(files[0]) as f:
+                for row in csv.DictReader(f):
+                    name, ctr = row["Kernel_Name"], row.get("Counter_Name", "")
+                    kind = next((k for k, match in kinds.items() if match(name)), None)
+                    if kind is None or ctr not in counters:
+                        continue
+                    acc[kind].setdefault(ctr, []).append(float(row["Counter_Value"]))
+                    if (kind, row["Dispatch_Id"]) not in seen:
+                        seen.add((kind, row["Dispatch_Id"]))
+                        durs[kind].append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+            for kind in acc:
+                for ctr in counters:
+                    if ctr not in acc[kind]:
+                        log(f"rocprofv3 pass {n}: {ctr} missing for the {kind} kernel")
+                        return None
+                    vals[kind][ctr] = float(np.mean(acc[kind][ctr]))
+    return {k: {"counters": vals[k], "us": float(np.mean(durs[k])), "dispatches": len(durs[k])} for k in kinds}
+
+
 def measure_traffic(timeout_s: int = 150) -> dict | None:
     """HBM bytes per matvec launch from the L2's memory requests counted by size:
     read = 32 RDREQ_32B + 64 RDREQ_64B + 128 RDREQ_128B, written = 64 WRREQ_64B +
@@ -639,45 +692,13 @@ def measure_traffic(timeout_s: int = 150) -> dict | None:
     the request is not counted as a bubble, which is where FETCH_SIZE's shortfall
     comes from.  The calibration dequantize (known bytes) checks the accounting.
     Returns None when rocprofv3 is unavailable or fails."""
-    import csv
-    import shutil
-    import subprocess
-    import tempfile
-
-    exe = shutil.which("rocprofv3")
-    if exe is None:
-        log("rocprofv3 not found: traffic not measured")
+    res = _pmc_passes(TRAFFIC_PASSES, ["--profile-pass"],
+                      {"matvec": lambda n: "gguf_mfma_stream" in n or "q4_matvec" in n,
+                       "cal": lambda n: "dequant_kernel" in n}, timeout_s)
+    if res is None:
+        log("traffic not measured")
         return None
-    vals: dict[str, dict[str, float]] = {"matvec": {}, "cal": {}}
-    env = dict(os.environ, TMPDIR="/tmp")
-    with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
-        for n, counters in enumerate(TRAFFIC_PASSES):
-            cmd = [exe, "--pmc", *counters, "--output-format", "csv", "-d", tmp, "-o", f"pass{n}", "--",
-                   sys.executable, str(ROOT / "bench.py"), "--profile-pass"]
-            try:
-                subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, check=True,
-                               stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
-            except (subprocess.SubprocessError, OSError) as e:
-                log(f"rocprofv3 pass {n} failed ({e}): traffic not measured")
-                return None
-            files = list(Path(tmp).rglob(f"pass{n}_counter_collection.csv"))
-            if not files:
-                log(f"rocprofv3 pass {n} wrote no counter file: traffic not measured")
-                return None
-            acc: dict[str, dict[str, list[float]]] = {"matvec": {}, "cal": {}}
-            with open(files[0]) as f:
-                for row in csv.DictReader(f):
-                    name, ctr = row["Kernel_Name"], row.get("Counter_Name", "")
-                    kind = ("matvec" if "gguf_mfma_stream" in name or "q4_matvec" in name
-                            else "cal" if "dequant_kernel" in name else None)
-                    if kind and ctr in counters:
-                        acc[kind].setdefault(ctr, []).append(float(row["Counter_Value"]))
-            for kind in acc:
-                for ctr in counters:
-                    if ctr not in acc[kind]:
-                        log(f"rocprofv3 pass {n}: {ctr} missing for the {kind} kernel")
-                        return None
-                    vals[kind][ctr] = float(np.mean(acc[kind][ctr]))
+    vals = {k: res[k]["counters"] for k in res}
 
     def account(v):
         read = 32 * v["TCC_EA0_RDREQ_32B_sum"] + 64 * v["TCC_EA0_RDREQ_64B_sum"] + 128 * v["TCC_EA0_RDREQ_128B_sum"]
@@ -700,6 +721,71 @@ def measure_traffic(timeout_s: int = 150) -> dict | None:
     }
 
 
+def gemm_profile_pass(T: int = 512, M: int = 11008, K: int = 4096, copies: int = 6, launches: int = 24) -> None:
+    """A short fixed GEMM workload for hardware-counter runs: `launches` Q8_0
+    GEMMs C[T][M] = A_q8[T][K] . W_q8[M][K]^T over rotating weight copies."""
+    from asmllm_amd import gguf, native
+    from asmllm_amd.device import DeviceBuffer, Stream
+
+    lib = native.lib()
+    wbufs, _ = _rotating_blocks(native.Q8_0, M, K, copies, seed=99)
+    dq = DeviceBuffer(gguf.q8_0_nbytes(T, K))
+    native.check(lib.asmhip_random_blocks(native.Q8_0, dq.ptr, T, K, 5, 1.0, None), "random activations")
+    dc = DeviceBuffer(4 * T * M)
+    stream = Stream()
+    for i in range(launches):
+        native.check(lib.asmhip_gemm_q8_0(wbufs[i % copies].ptr, dq.ptr, dc.ptr, T, M, K, stream.handle), "gemm")
+    stream.synchronize()
+    log(f"GEMM profile pass: {launches} launches ({T}x{M}x{K})")
+
+
+# rocprofv3 passes for the GEMM (each within one pass's limit of 8 SQ and 2 GRBM
+# counters): matrix-core and VALU issue, then the VALU mix, LDS and waits
+GEMM_PASSES = (
+    ("SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU", "SQ_INSTS_VALU_MFMA_MOPS_I8", "SQ_INSTS_MFMA",
+     "SQ_ACTIVE_INST_VALU", "SQ_WAVES", "SQ_INSTS_LDS", "GRBM_GUI_ACTIVE"),
+    ("SQ_INSTS_VALU_CVT", "SQ_INSTS_VALU_FMA_F32", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAIT_INST_ANY",
+     "SQ_WAVE_CYCLES", "SQ_INSTS_SALU", "SQ_INSTS_VALU_MFMA_MOPS_F16", "GRBM_GUI_ACTIVE"),
+)
+
+
+def gemm_counters(T: int = 512, M: int = 11008, K: int = 4096, timeout_s: int = 150) -> dict | None:
+    """Hardware counters of the Q8_0 GEMM per dispatch and what they give:
+    matrix-core busy fraction, int8 ops counted by the hardware (MOPS_I8 x 512)
+    against 2 T M K, VALU instructions per 32x32 output tile and block, the shader
+    clock (GUI-active cycles per XCD over the dispatch's duration)."""
+    from asmllm_amd.device import device_info
+
+    res = _pmc_passes(GEMM_PASSES, ["--gemm-profile-pass"], {"gemm": lambda n: "gemm_q8_0" in n}, timeout_s)
+    if res is None:
+        return None
+    v, us = res["gemm"]["counters"], res["gemm"]["us"]
+    cus = device_info()["compute_units"]
+    simds, xcds = 4 * cus, 8
+    gui = v["GRBM_GUI_ACTIVE"] / xcds  # summed over the XCDs' GRBMs
+    block_tiles = (T // 32) * (M // 32) * (K // 32)
+    ops = 2 * T * M * K
+    return {
+        "workload": f"Q8_0 GEMM C[{T}][{M}] = A_q8[{T}][{K}] . W_q8[{M}][{K}]^T, eager launches",
+        "dispatch_us": round(us, 3),
+        "dispatches": res["gemm"]["dispatches"],
+        "counters": {k: round(x, 1) for k, x in v.items()},
+        "gui_cycles": round(gui, 0),
+        "shader_clock_ghz": round(gui / us / 1e3, 3),
+        "mfma_busy_frac": round(v["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * simds), 4),
+        "int8_ops_counted": v["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512,
+        "int8_ops_expected": ops,
+        "int8_TOPs": round(ops / us / 1e6, 1),
+        "valu_insts_per_block_tile": round(v["SQ_INSTS_VALU"] / block_tiles, 2),
+        "cvt_per_block_tile": round(v["SQ_INSTS_VALU_CVT"] / block_tiles, 2),
+        "fma_f32_per_block_tile": round(v["SQ_INSTS_VALU_FMA_F32"] / block_tiles, 2),
+        "mfma_per_block_tile": round(v["SQ_INSTS_MFMA"] / block_tiles, 2),
+        "lds_insts_per_block_tile": round(v["SQ_INSTS_LDS"] / block_tiles, 2),
+        "valu_issue_frac": round(4 * v["SQ_INSTS_VALU"] / (gui * simds), 4),
+        "lds_bank_conflict_frac_of_lds_active": round(v["SQ_LDS_BANK_CONFLICT"] / max(v["SQ_LDS_IDX_ACTIVE"], 1), 4),
+    }
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -710,9 +796,11 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-pass", action="store_true",
                     help="run only a short fixed workload for hardware-counter collection")
+    ap.add_argument("--gemm-profile-pass", action="store_true",
+                    help="run only a short fixed GEMM workload for hardware-counter collection")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-extra", action="store_true", help="skip the shape table, GEMM and decode legs")
-    ap.add_argument("--only", choices=["decode", "gemm", "table", "floor", "host", "cpu", "traffic"],
+    ap.add_argument("--only", choices=["decode", "gemm", "table", "floor", "host", "cpu", "traffic", "gemm_counters"],
                     help="run one extra leg and print its JSON")
     ap.add_argument("--eager", action="store_true", help="with --only: launch without graphs")
     args = ap.parse_args()
@@ -723,6 +811,9 @@ def main() -> None:
 
     if args.profile_pass:
         profile_pass(args.copies)
+        return
+    if args.gemm_profile_pass:
+        gemm_profile_pass()
         return
 
     from asmllm_amd.device import device_info
@@ -736,7 +827,8 @@ def main() -> None:
             res = bench_cpu_baseline(args.cpu_seconds)
         else:
             res = {"gemm": bench_gemm, "table": bench_matvec_table, "floor": bench_read_floor,
-                   "host": bench_host_pointer, "traffic": measure_traffic}[args.only]()
+                   "host": bench_host_pointer, "traffic": measure_traffic,
+                   "gemm_counters": gemm_counters}[args.only]()
         print(json.dumps({args.only: res}), flush=True)
         return
 
