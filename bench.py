@@ -473,6 +473,49 @@ def bench_read_floor(multiples=(1, 2, 4, 8)) -> dict:
             "floor_frac_of_peak": round(points[0]["GBps"] / HBM_PEAK_GBPS, 4)}
 
 
+def bench_matvec_phases(K: int = K_MAIN, rows=(1024, 2048, 4096, 8192, 11008, 16384, 22016, 32000),
+                        min_rotated_bytes: int = 600_000_000) -> dict:
+    """Ramp and tail against the steady stream of the Q4_0 matvec: the same kernel
+    (K = 4096) timed at several row counts, weights rotating over >= 32 copies and
+    >= 600 MB, and a straight-line fit of time against bytes over the rows that
+    fill the grid (M >= 4096: one 16-row tile or more per compute unit).  The
+    slope is the steady streaming rate; the intercept is what a launch costs
+    besides streaming (dispatch, x read and digitization before the first
+    multiply, the last tiles' tail, the partial-sum reduction and store).  Set
+    beside the read floor's fit (`--only floor`) it says whether the gap to the
+    floor is rate or fixed cost."""
+    from asmllm_amd import native
+    from asmllm_amd.device import DeviceBuffer
+
+    lib = native.lib()
+    points = []
+    for M in rows:
+        nbytes_w = M * (K // 32) * 18
+        copies = max(32, -(-min_rotated_bytes // nbytes_w))
+        bufs, _ = _rotating_blocks(native.Q4_0, M, K, copies, seed=M + 5)
+        dx, dy = DeviceBuffer(4 * K), DeviceBuffer(4 * M)
+        native.check(lib.asmhip_fill_f32(dx.ptr, K, 0.5, None), "fill")
+
+        def enqueue(i, st, bufs=bufs, dx=dx, dy=dy, M=M):
+            native.check(lib.asmhip_matmul_q4_0(bufs[i % len(bufs)].ptr, dx.ptr, dy.ptr, M, K, st), "matvec")
+
+        us = time_launches(enqueue, copies, reps=max(4, 4000 // copies))
+        algo = q4_algorithmic_bytes(M, K)
+        points.append({"M": M, "bytes": algo, "us": round(us, 3), "GBps": round(algo / us / 1e3, 1)})
+        log(f"matvec {M}x{K}: {us:.3f} us, {algo / us / 1e3:.0f} GB/s")
+        for b in bufs:
+            b.close()
+        dx.close()
+        dy.close()
+    full = [p for p in points if p["M"] >= 4096]
+    xs = np.array([p["bytes"] for p in full], np.float64)
+    ys = np.array([p["us"] for p in full], np.float64)
+    slope, fixed = np.polyfit(xs, ys, 1)
+    resid = ys - (fixed + slope * xs)
+    return {"K": K, "points": points, "fit_rows": "M >= 4096", "fixed_us_per_launch": round(float(fixed), 3),
+            "steady_GBps": round(1e-3 / float(slope), 1), "fit_max_residual_us": round(float(np.max(np.abs(resid))), 3)}
+
+
 INT8_MFMA_PEAK_TOPS = 5000.0
 
 
@@ -816,7 +859,8 @@ def main() -> None:
                     help="run only a short fixed GEMM workload for hardware-counter collection")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-extra", action="store_true", help="skip the shape table, GEMM and decode legs")
-    ap.add_argument("--only", choices=["decode", "gemm", "table", "floor", "host", "cpu", "traffic", "gemm_counters"],
+    ap.add_argument("--only", choices=["decode", "gemm", "table", "floor", "host", "cpu", "traffic", "gemm_counters",
+                                       "phases"],
                     help="run one extra leg and print its JSON")
     ap.add_argument("--eager", action="store_true", help="with --only: launch without graphs")
     args = ap.parse_args()
@@ -844,7 +888,7 @@ def main() -> None:
         else:
             res = {"gemm": bench_gemm, "table": bench_matvec_table, "floor": bench_read_floor,
                    "host": bench_host_pointer, "traffic": measure_traffic,
-                   "gemm_counters": gemm_counters}[args.only]()
+                   "gemm_counters": gemm_counters, "phases": bench_matvec_phases}[args.only]()
         print(json.dumps({args.only: res}), flush=True)
         return
 
