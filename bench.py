@@ -465,12 +465,21 @@ def bench_read_floor(multiples=(1, 2, 4, 8)) -> dict:
     xs = np.array([p["bytes"] for p in points], np.float64)
     ys = np.array([p["us"] for p in points], np.float64)
     slope, fixed = np.polyfit(xs, ys, 1)
+
+    # the same kernel on 4 KB (one 16-byte load per workgroup): what a dependent
+    # graph node costs with next to no work, in graphs of 64 launches
+    def enqueue_tiny(i, st):
+        native.check(lib.asmhip_stream_read(buf.ptr + i * 4096, 4096, sink.ptr, st), "stream read")
+
+    launch_us = time_launches(enqueue_tiny, 64, reps=50)
+    log(f"stream read 4 KB (launch floor): {launch_us:.3f} us")
     buf.close()
     sink.close()
     return {"points": points, "fixed_us_per_launch": round(float(fixed), 3),
             "sustained_GBps": round(1e-3 / float(slope), 1),
             "floor_us_at_matvec_bytes": points[0]["us"],
-            "floor_frac_of_peak": round(points[0]["GBps"] / HBM_PEAK_GBPS, 4)}
+            "floor_frac_of_peak": round(points[0]["GBps"] / HBM_PEAK_GBPS, 4),
+            "launch_floor_us_4KB": round(launch_us, 3)}
 
 
 def bench_matvec_phases(K: int = K_MAIN, rows=(1024, 2048, 4096, 8192, 11008, 16384, 22016, 32000),
