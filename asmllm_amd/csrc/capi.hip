@@ -624,6 +624,53 @@ extern "C" int asmhip_attention_decode_rope_table(const float* qkv, void* k_cach
                               true, 0.f, (hipStream_t)stream, rope_table);
 }
 
+extern "C" int asmhip_attention_decode_partials_rope_table(const float* qkv, void* k_cache, void* v_cache,
+                                                           float* workspace, int n_heads, int n_kv_heads,
+                                                           int head_dim, const int* pos_dev, int max_ctx,
+                                                           const float* rope_table, void* stream) {
+    if (!qkv || !k_cache || !v_cache || !workspace || !pos_dev || !rope_table)
+        return fail(kInvalidArgument, "null pointer argument");
+    if (n_heads <= 0 || max_ctx <= 0 || head_dim % 2) return fail(kInvalidArgument, "bad attention shape");
+    return attn_decode_launch(qkv, k_cache, v_cache, workspace, nullptr, n_heads, n_kv_heads, head_dim, pos_dev,
+                              max_ctx, true, 0.f, (hipStream_t)stream, rope_table);
+}
+
+extern "C" int asmhip_matmul_attn_output(int qtype, const void* blocks, const float* workspace, float* work, float* y,
+                                         int64_t M, int n_heads, int head_dim, int max_ctx, int accumulate,
+                                         void* stream) {
+    QuantType qt;
+    int rc = check_ptrs(blocks, workspace, y);
+    if (!rc && !work) rc = fail(kInvalidArgument, "null pointer argument");
+    if (!rc) rc = quant_type(qtype, &qt);
+    if (rc) return rc;
+    if (n_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return fail(kInvalidArgument, "bad attention shape");
+    const int splits = attn_decode_splits(max_ctx);
+    if (splits > kAttnMaxSplits)
+        return fail(kUnsupported, "attention output: max_ctx %d exceeds %d positions", max_ctx,
+                    kAttnMaxSplits * kAttnSplitLen);
+    const int64_t K = (int64_t)n_heads * head_dim;
+    const hipStream_t st = (hipStream_t)stream;
+    MatvecOpts o;
+    o.pre = kPreAttnMerge;
+    o.pre_arg = workspace;
+    o.accumulate = accumulate != 0;
+    o.attn_splits = splits;
+    o.attn_hd = head_dim;
+    // one launch where the int8-MFMA stream takes the shape: the merge is its x prologue
+    if (get_q4_kernel() != kQ4KernelFp32) {
+        if (qt == QuantType::Q4_0 && q4_0_mfma_eligible(blocks, workspace, o, M, K))
+            return q4_0_mfma_launch(blocks, workspace, y, M, K, st, o);
+        if (qt == QuantType::Q8_0 && q8_0_mfma_eligible(blocks, workspace, o, M, K))
+            return q8_0_mfma_launch(blocks, workspace, y, M, K, st, o);
+    }
+    // otherwise the merge launch into `work`, then the matvec over it
+    rc = attn_merge_launch(workspace, work, n_heads, head_dim, max_ctx, st);
+    if (rc) return rc;
+    MatvecOpts p;
+    p.accumulate = o.accumulate;
+    return matvec_launch(qt, true, blocks, nullptr, work, y, M, K, st, p);
+}
+
 // ---- decode attention without a caller workspace -----------------------------------------
 //
 // For callers that cannot allocate (graph capture, tight serving loops): the
@@ -636,7 +683,7 @@ extern "C" int asmhip_attention_decode_rope_table(const float* qkv, void* k_cach
 // nothing needs clearing between calls; calls that overlap on one GPU share the
 // array and race.
 namespace {
-constexpr int64_t kNoAllocScratchFloats = 1 << 20;  // 4 MiB: n_heads * ceil(max_ctx / 128) * (head_dim + 2)
+constexpr int64_t kNoAllocScratchFloats = 1 << 20;  // 4 MiB: n_heads * ceil(max_ctx / 512) * (head_dim + 4)
 __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 float* g_scratch_ptr[kMaxDevices] = {};
 
@@ -671,7 +718,7 @@ extern "C" int asmhip_attention_decode_rope_noalloc(const float* qkv, void* k_ca
     const int64_t need = attn_decode_workspace(n_heads, head_dim, max_ctx);
     if (need > kNoAllocScratchFloats)
         return fail(kInvalidArgument,
-                    "attention without a workspace: n_heads %d x %d splits x (head_dim %d + 2) = %lld floats "
+                    "attention without a workspace: n_heads %d x %d splits x (head_dim %d + 4) = %lld floats "
                     "exceeds the %lld-float scratch; pass a workspace to asmhip_attention_decode_rope",
                     n_heads, attn_decode_splits(max_ctx), head_dim, (long long)need,
                     (long long)kNoAllocScratchFloats);

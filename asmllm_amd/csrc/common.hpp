@@ -92,4 +92,67 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Softmax merge of the S split states of one attention head, dimension t:
+// state s is [m, l, -, -, acc[hd]] at ph + s * stride; the result is
+// (sum_s acc_s[t] f_s) / (sum_s l_s f_s) with f_s = exp(m_s - max_s m_s), both
+// sums in split order; 0 when no split saw a position (every m = -inf).
+__device__ __forceinline__ float attn_merge_value(const float* ph, int S, int stride, int t) {
+    float M = -INFINITY;
+    for (int i = 0; i < S; ++i) M = fmaxf(M, ph[(size_t)i * stride]);
+    float L = 0.f, a = 0.f;
+    if (M != -INFINITY) {
+        for (int i = 0; i < S; ++i) {
+            const float f = __expf(ph[(size_t)i * stride] - M);
+            L = fmaf(ph[(size_t)i * stride + 1], f, L);
+            a = fmaf(ph[(size_t)i * stride + 4 + t], f, a);
+        }
+    }
+    return M == -INFINITY ? 0.f : a / L;
+}
+
+// attn_merge_value for the dimensions t..t+3 and t+16..t+19 of one head (t % 4
+// == 0, stride % 4 == 0, ph 16-byte aligned) over exactly S splits, bit for bit
+// the same values, in two steps: load() requests every state with
+// unconditional loads (so the wait before finish() counts them exactly),
+// finish() forms the values once they are in.
+template <int S>
+struct AttnMergeQuads {
+    float2 ml[S];
+    float4 ac[S][2];
+
+    __device__ __forceinline__ void load(const float* ph, int stride, int t) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const float* e = ph + (size_t)i * stride;
+            ml[i] = *reinterpret_cast<const float2*>(e);
+            ac[i][0] = *reinterpret_cast<const float4*>(e + 4 + t);
+            ac[i][1] = *reinterpret_cast<const float4*>(e + 20 + t);
+        }
+    }
+
+    __device__ __forceinline__ void finish(float4* lo, float4* hi) const {
+        float M = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < S; ++i) M = fmaxf(M, ml[i].x);
+        float L = 0.f;
+        float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const float f = __expf(ml[i].x - M);
+                L = fmaf(ml[i].y, f, L);
+                const float v[8] = {ac[i][0].x, ac[i][0].y, ac[i][0].z, ac[i][0].w,
+                                    ac[i][1].x, ac[i][1].y, ac[i][1].z, ac[i][1].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) a[j] = fmaf(v[j], f, a[j]);
+            }
+        }
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = M == -INFINITY ? 0.f : a[j] / L;
+        *lo = make_float4(r[0], r[1], r[2], r[3]);
+        *hi = make_float4(r[4], r[5], r[6], r[7]);
+    }
+};
+
 }  // namespace asmhip

@@ -201,22 +201,26 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(const float* __restri
 // grid (n_heads, S = ceil(max_ctx / kAttnSplitLen)); workgroup (h, s) covers
 // positions [s*kAttnSplitLen, (s+1)*kAttnSplitLen) of 0..pos.  Within a workgroup
 // a position is read by HD/8 lanes (8 dims = 16 bytes each), so a wave covers
-// 64/(HD/8) positions per row and the four waves kRowPos; every k and v load of
-// the workgroup is issued before the first score is formed (q, then every k
-// row, then every v row).  Each lane group keeps a softmax state (max m, sum l,
-// acc[8]) over its positions; the states of all lane groups of the workgroup
-// merge once through LDS; each workgroup writes
-// [m, l, acc[HD]] to `part`, and attn_decode_merge combines the S partials of a
-// head in split order into out = acc / l.
+// 64/(HD/8) positions per row and the four waves kRowPos; a lane reads
+// kAttnRows rows of k and of v per chunk (one position each), and the split is
+// kChunks chunks walked with the next chunk's loads in flight while the current
+// one is scored (two register buffers).  k and v are read with nontemporal
+// loads: the cache rows are read once per token.  Each lane group keeps an
+// online softmax state (max m, sum l, acc[8]) over its positions; the states of
+// all lane groups of the workgroup merge once through LDS; each workgroup
+// writes [m, l, -, -, acc[HD]] (kAttnPartStride(HD) floats, acc 16-byte
+// aligned) to `part`, and attn_decode_merge, or a matvec whose x is the
+// attention output (kPreAttnMerge), combines the S partials of a head in split
+// order into acc / l (attn_merge_value).
 //
 // ROPE != kRopeNone also does what rope_kv_write does, inside the same launch:
 // q and the new k are rotated at `pos`, the new k and v are rounded to fp16 and
 // written to the caches at `pos` (by the workgroup of the first query head of
-// the kv group), and the workgroup whose split holds `pos` uses those fp16
-// values instead of reading the row it writes.  kRopeTheta forms the angles
-// (rope_angle, double precision: about 600 fp64 instructions that every wave
-// waits for); kRopeTable reads the same cos/sin values from a table that
-// rope_table_kernel filled once, a load that travels with the k/v loads.
+// the kv group), and the lane that owns `pos` uses those fp16 values instead of
+// reading the row it writes.  kRopeTheta forms the angles (rope_angle, double
+// precision: about 600 fp64 instructions that every wave waits for); kRopeTable
+// reads the same cos/sin values from a table that rope_table_kernel filled
+// once, a load that travels with the k/v loads.
 // Sum over aligned groups of N lanes (N = 8 or 16), every lane receiving its
 // group's sum, with DPP adds instead of LDS permutes: quad_perm [1,0,3,2] and
 // [2,3,0,1] sum the quads, row_half_mirror pairs quad 0 with 1 (2 with 3),
@@ -277,13 +281,16 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     static_assert(HD == E * kLanes && kWave % kLanes == 0, "head_dim 48, 64 or 128");
     constexpr int kGroups = kWave / kLanes;               // positions per wave and row
     constexpr int kRowPos = kGroups * (kBlock / kWave);   // positions per workgroup and row
-    constexpr int kRows = kAttnSplitLen / kRowPos;
-    static_assert(kAttnSplitLen % kRowPos == 0, "split must hold whole rows");
+    constexpr int R = kAttnRows;                          // rows per lane and chunk
+    constexpr int kChunkPos = kRowPos * R;
+    constexpr int kChunks = kAttnSplitLen / kChunkPos;
+    static_assert(kAttnSplitLen % kChunkPos == 0, "split must hold whole chunks");
+    constexpr int kStride = kAttnPartStride(HD);
     __shared__ float cs[HD];                 // cos, sin of pair i at 2i, 2i+1
     constexpr int kGroupsWg = kBlock / kLanes;  // lane groups (position slots) of the workgroup
     __shared__ float wst[kGroupsWg][HD + 2];
 
-    const int h = blockIdx.x, split = blockIdx.y, S = gridDim.y;
+    const int h = blockIdx.x, split = blockIdx.y;
     const int group = n_heads / n_kv, kvh = h / group;
     const int pos = *pos_ptr;
     const int n_pos = (pos >= 0 && pos < max_ctx) ? pos + 1 : 0;  // an invalid position reads and writes nothing
@@ -291,11 +298,13 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
     const int g = lane / kLanes, c = lane % kLanes;
     const size_t head_off = (size_t)kvh * max_ctx * HD + E * c;
+    // position of row r of chunk ch for this lane
+    auto position = [&](int ch, int r) { return p0 + ch * kChunkPos + r * kRowPos + w * kGroups + g; };
 
-    // q first, then all k rows of this lane, then all v rows: loads return in
+    // q first, then the first chunk's k rows, then its v rows: loads return in
     // order, so the scores can start while v is in flight.  HD % 64 == 0:
-    // branch-free buffer loads, a row outside the split reading zeros from past
-    // the end of the buffer.
+    // branch-free buffer loads, a row outside the split (or the row at pos,
+    // which this launch writes) reading zeros from past the end of the buffer.
     float qv[E];
 #pragma unroll
     for (int t = 0; t < E; t += 2) {
@@ -312,31 +321,35 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
             csl[t] = a.x, csl[t + 1] = a.y;
         }
     }
-    HalfRow<E> kr[kRows], vr[kRows];
+    constexpr int NB = kChunks > 1 ? 2 : 1;
+    HalfRow<E> kr[NB][R], vr[NB][R];
     const uint32_t cache_bytes = (uint32_t)n_kv * (uint32_t)max_ctx * (uint32_t)(2 * HD);  // < 4 GB, checked at launch
     const auto kres = make_rsrc(kc, cache_bytes), vres = make_rsrc(vc, cache_bytes);
-    uint32_t off[kRows];
+    auto issue = [&](int b, int ch) {
+        uint32_t off[R];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        const int p = p0 + r * kRowPos + w * kGroups + g;
-        const bool live = p < p1 && !(ROPE != kRopeNone && p == pos);
-        off[r] = live ? 2u * (uint32_t)(head_off + (size_t)p * HD) : kAttnPastEnd;
-        if constexpr (E == 8) {
-            const uint4 a = buf_load_b128(kres, off[r]);
-            kr[r].w[0] = a.x, kr[r].w[1] = a.y, kr[r].w[2] = a.z, kr[r].w[3] = a.w;
-        } else {
-            kr[r] = live ? HalfRow<E>::load(kc + head_off + (size_t)p * HD) : HalfRow<E>::zero();
+        for (int r = 0; r < R; ++r) {
+            const int p = position(ch, r);
+            const bool live = p < p1 && !(ROPE != kRopeNone && p == pos);
+            off[r] = live ? 2u * (uint32_t)(head_off + (size_t)p * HD) : kAttnPastEnd;
+            if constexpr (E == 8) {
+                const uint4 a = buf_load_b128_nt(kres, off[r]);
+                kr[b][r].w[0] = a.x, kr[b][r].w[1] = a.y, kr[b][r].w[2] = a.z, kr[b][r].w[3] = a.w;
+            } else {
+                kr[b][r] = live ? HalfRow<E>::load(kc + off[r] / 2) : HalfRow<E>::zero();
+            }
         }
-    }
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        if constexpr (E == 8) {
-            const uint4 b = buf_load_b128(vres, off[r]);
-            vr[r].w[0] = b.x, vr[r].w[1] = b.y, vr[r].w[2] = b.z, vr[r].w[3] = b.w;
-        } else {
-            vr[r] = off[r] != kAttnPastEnd ? HalfRow<E>::load(vc + off[r] / 2) : HalfRow<E>::zero();
+        for (int r = 0; r < R; ++r) {
+            if constexpr (E == 8) {
+                const uint4 a = buf_load_b128_nt(vres, off[r]);
+                vr[b][r].w[0] = a.x, vr[b][r].w[1] = a.y, vr[b][r].w[2] = a.z, vr[b][r].w[3] = a.w;
+            } else {
+                vr[b][r] = off[r] != kAttnPastEnd ? HalfRow<E>::load(vc + off[r] / 2) : HalfRow<E>::zero();
+            }
         }
-    }
+    };
+    issue(0, 0);
     if constexpr (ROPE == kRopeTheta) {
         if (threadIdx.x < HD / 2 && n_pos > 0)
             rope_angle(threadIdx.x, HD, pos, theta, &cs[2 * threadIdx.x], &cs[2 * threadIdx.x + 1]);
@@ -344,16 +357,18 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
 #pragma unroll
         for (int t = 0; t < E; ++t) csl[t] = cs[E * c + t];
     }
+    // the new row: rotated k and v of kv head kvh, rounded to fp16, used by
+    // the lane that owns position pos (chunk nch, row nr)
+    HalfRow<E> kq = HalfRow<E>::zero(), vq = HalfRow<E>::zero();
+    int nch = -1, nr = -1;
     if constexpr (ROPE != kRopeNone) {
         if (n_pos > 0) {
 #pragma unroll
             for (int i = 0; i < E / 2; ++i) rotate(&qv[2 * i], csl[2 * i], csl[2 * i + 1]);
         }
         if (p0 <= pos && pos < p1) {
-            // the new row: rotated k and v of kv head kvh, rounded to fp16
             const float* kn = qkv + (size_t)(n_heads + kvh) * HD + E * c;
             const float* vn = qkv + (size_t)(n_heads + n_kv + kvh) * HD + E * c;
-            HalfRow<E> kq, vq;
 #pragma unroll
             for (int i = 0; i < E / 2; ++i) {
                 float kk[2] = {kn[2 * i], kn[2 * i + 1]};
@@ -363,11 +378,10 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
                 vq.w[i] = (uint32_t)__half_as_ushort(__float2half_rn(vn[2 * i])) |
                           ((uint32_t)__half_as_ushort(__float2half_rn(vn[2 * i + 1])) << 16);
             }
-            const int rr = (pos - p0) / kRowPos, rem = (pos - p0) % kRowPos;
+            const int rel = pos - p0, rem = rel % kRowPos;
             if (w == rem / kGroups && g == rem % kGroups) {
-#pragma unroll
-                for (int r = 0; r < kRows; ++r)
-                    if (r == rr) kr[r] = kq, vr[r] = vq;
+                nch = rel / kChunkPos;
+                nr = (rel % kChunkPos) / kRowPos;
                 if (h % group == 0) {
                     kq.store(kc + head_off + (size_t)pos * HD);
                     vq.store(vc + head_off + (size_t)pos * HD);
@@ -379,35 +393,51 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
 #pragma unroll
     for (int t = 0; t < E; ++t) qv[t] *= scale;
 
-    // scores of this lane group's positions, then its softmax state
-    float sc[kRows];
-    float m = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        float d = 0.f;
-#pragma unroll
-        for (int t = 0; t < E / 2; ++t) {
-            d = fmaf(qv[2 * t], half_lo(kr[r].w[t]), d);
-            d = fmaf(qv[2 * t + 1], half_hi(kr[r].w[t]), d);
-        }
-        d = group_sum<kLanes>(d);
-        const int p = p0 + r * kRowPos + w * kGroups + g;
-        sc[r] = p < p1 ? d : -INFINITY;
-        m = fmaxf(m, sc[r]);
-    }
-    float l = 0.f, acc[E];
+    // chunk by chunk: request the next chunk, then score this one and fold it
+    // into the lane group's online softmax state
+    float m = -INFINITY, l = 0.f, acc[E];
 #pragma unroll
     for (int t = 0; t < E; ++t) acc[t] = 0.f;
-    if (m != -INFINITY) {
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-            const float e = __expf(sc[r] - m);  // 0 for positions past the split
-            l += e;
+    for (int ch = 0; ch < kChunks; ++ch) {
+        const int b = NB > 1 ? (ch & 1) : 0;
+        if (ch + 1 < kChunks) issue((ch + 1) & 1, ch + 1);
+        if (ch == nch) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (r == nr) kr[b][r] = kq, vr[b][r] = vq;
+        }
+        float sc[R];
+        float mc = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float d = 0.f;
 #pragma unroll
             for (int t = 0; t < E / 2; ++t) {
-                acc[2 * t] = fmaf(e, half_lo(vr[r].w[t]), acc[2 * t]);
-                acc[2 * t + 1] = fmaf(e, half_hi(vr[r].w[t]), acc[2 * t + 1]);
+                d = fmaf(qv[2 * t], half_lo(kr[b][r].w[t]), d);
+                d = fmaf(qv[2 * t + 1], half_hi(kr[b][r].w[t]), d);
             }
+            d = group_sum<kLanes>(d);
+            sc[r] = position(ch, r) < p1 ? d : -INFINITY;
+            mc = fmaxf(mc, sc[r]);
+        }
+        const float mn = fmaxf(m, mc);
+        if (mn != -INFINITY) {
+            const float f = __expf(m - mn);  // 0 while the state is empty
+            l *= f;
+#pragma unroll
+            for (int t = 0; t < E; ++t) acc[t] *= f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float e = __expf(sc[r] - mn);  // 0 for positions past the split
+                l += e;
+#pragma unroll
+                for (int t = 0; t < E / 2; ++t) {
+                    acc[2 * t] = fmaf(e, half_lo(vr[b][r].w[t]), acc[2 * t]);
+                    acc[2 * t + 1] = fmaf(e, half_hi(vr[b][r].w[t]), acc[2 * t + 1]);
+                }
+            }
+            m = mn;
         }
     }
     // every lane group's softmax state to LDS (no cross-lane shuffles), then one
@@ -420,7 +450,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
         if (c == 0) wst[gs][0] = m, wst[gs][1] = l;
     }
     __syncthreads();
-    float* mine = part + ((size_t)h * S + split) * (HD + 2);
+    float* mine = part + ((size_t)h * gridDim.y + split) * kStride;
     if (threadIdx.x < HD) {
         float M = -INFINITY;
 #pragma unroll
@@ -434,7 +464,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
                 a = fmaf(wst[i][2 + threadIdx.x], f, a);
             }
         }
-        mine[2 + threadIdx.x] = a;
+        mine[4 + threadIdx.x] = a;
         if (threadIdx.x == 0) mine[0] = M, mine[1] = L;
     }
 }
@@ -444,27 +474,9 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_decode_merge(const float* __restrict__ part, float* __restrict__ out,
                                                         int S) {
-    __shared__ float sm[64], sl[64];
     const int h = blockIdx.x;
-    const float* ph = part + (size_t)h * S * (HD + 2);
-    for (int i = threadIdx.x; i < S; i += HD) {  // S <= 64, checked at launch
-        sm[i] = ph[(size_t)i * (HD + 2)];
-        sl[i] = ph[(size_t)i * (HD + 2) + 1];
-    }
-    __syncthreads();
-    float M = -INFINITY;
-    for (int i = 0; i < S; ++i) M = fmaxf(M, sm[i]);
-    float L = 0.f, a = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll 8
-        for (int i = 0; i < S; ++i) {
-            const float f = __expf(sm[i] - M);
-            L = fmaf(sl[i], f, L);
-            a = fmaf(ph[(size_t)i * (HD + 2) + 2 + threadIdx.x], f, a);
-        }
-    }
-    // no position in range (pos outside [0, max_ctx)): a defined zero instead of 0 / 0
-    out[(size_t)h * HD + threadIdx.x] = M == -INFINITY ? 0.f : a / L;
+    out[(size_t)h * HD + threadIdx.x] = attn_merge_value(part + (size_t)h * S * kAttnPartStride(HD), S,
+                                                         kAttnPartStride(HD), threadIdx.x);
 }
 
 // ---- embedding row of a Q4_0 table -----------------------------------------------------
@@ -617,7 +629,7 @@ int attention_launch(const float* q, const float* k, const float* v, float* y, i
 int attn_decode_splits(int max_ctx) { return (max_ctx + kAttnSplitLen - 1) / kAttnSplitLen; }
 
 int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx) {
-    return (int64_t)n_heads * attn_decode_splits(max_ctx) * (hd + 2);
+    return (int64_t)n_heads * attn_decode_splits(max_ctx) * kAttnPartStride(hd);
 }
 
 namespace {
@@ -634,7 +646,7 @@ void launch_attn_decode(int mode, dim3 grid, hipStream_t st, const float* qkv, _
     else
         hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeNone>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
                            n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
-    hipLaunchKernelGGL((attn_decode_merge<HD>), dim3(n_heads), dim3(HD), 0, st, part, out, (int)grid.y);
+    if (out) hipLaunchKernelGGL((attn_decode_merge<HD>), dim3(n_heads), dim3(HD), 0, st, part, out, (int)grid.y);
 }
 }  // namespace
 
@@ -644,10 +656,11 @@ int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* pa
     if (n_kv <= 0 || n_heads % n_kv) return fail(kInvalidArgument, "attention: n_heads %% n_kv_heads != 0");
     if (max_ctx <= 0) return fail(kInvalidArgument, "attention: max_ctx must be > 0");
     const int splits = attn_decode_splits(max_ctx);
-    if (splits > 64)
-        return fail(kUnsupported, "attention: max_ctx %d exceeds %d positions", max_ctx, 64 * kAttnSplitLen);
-    if ((uintptr_t)qkv % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
-        return fail(kInvalidArgument, "attention: q and the caches must be 16-byte aligned");
+    if (splits > kAttnMaxSplits)
+        return fail(kUnsupported, "attention: max_ctx %d exceeds %d positions", max_ctx,
+                    kAttnMaxSplits * kAttnSplitLen);
+    if ((uintptr_t)qkv % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 || (uintptr_t)part % 16)
+        return fail(kInvalidArgument, "attention: q, the caches and the workspace must be 16-byte aligned");
     if (rope_table && (uintptr_t)rope_table % 8)
         return fail(kInvalidArgument, "attention: the RoPE table must be 8-byte aligned");
     if ((int64_t)n_kv * max_ctx * hd * 2 >= (int64_t)kAttnPastEnd)
@@ -667,6 +680,24 @@ int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* pa
                                rope_table);
     else
         return fail(kUnsupported, "attention: head_dim %d (supported: 48, 64, 128)", hd);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int attn_merge_launch(const float* part, float* out, int n_heads, int hd, int max_ctx, hipStream_t st) {
+    if (n_heads <= 0 || max_ctx <= 0) return fail(kInvalidArgument, "attention merge: bad shape");
+    const int splits = attn_decode_splits(max_ctx);
+    if (splits > kAttnMaxSplits)
+        return fail(kUnsupported, "attention merge: max_ctx %d exceeds %d positions", max_ctx,
+                    kAttnMaxSplits * kAttnSplitLen);
+    if (hd == 128)
+        hipLaunchKernelGGL((attn_decode_merge<128>), dim3(n_heads), dim3(128), 0, st, part, out, splits);
+    else if (hd == 64)
+        hipLaunchKernelGGL((attn_decode_merge<64>), dim3(n_heads), dim3(64), 0, st, part, out, splits);
+    else if (hd == 48)
+        hipLaunchKernelGGL((attn_decode_merge<48>), dim3(n_heads), dim3(48), 0, st, part, out, splits);
+    else
+        return fail(kUnsupported, "attention merge: head_dim %d (supported: 48, 64, 128)", hd);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

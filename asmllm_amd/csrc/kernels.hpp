@@ -16,6 +16,12 @@ enum PreOp : int {
     kPreNone = 0,
     kPreRmsNorm = 1,  // x <- (x * 1/sqrt(mean(x^2) + eps)) * arg[k]
     kPreSwiGlu = 2,   // x <- x / (1 + exp(-x)) * arg[k]
+    // x is the decode attention output, merged from its split partials: arg is
+    // the [n_heads][attn_splits][kAttnPartStride(attn_hd)] workspace that
+    // attn_decode_launch(..., out = nullptr) filled, K = n_heads * attn_hd
+    // (x itself is not read).  Q4_0 int8-MFMA stream only, attn_splits <=
+    // kAttnMergeMaxSplits.
+    kPreAttnMerge = 3,
 };
 
 // Work fused into a matvec's write of y.  kPostSwiGlu8: the rows of W come in
@@ -32,6 +38,8 @@ struct MatvecOpts {
     float eps = 0.f;
     bool accumulate = false;  // y += W x
     int post = kPostNone;
+    int attn_splits = 0;      // kPreAttnMerge: splits per head and head_dim
+    int attn_hd = 0;
 };
 
 // y = W x.  gguf: W is [M][K/32] GGUF blocks; otherwise W is the split qs
@@ -112,10 +120,17 @@ int attention_launch(const float* q, const float* k, const float* v, float* y, i
                      hipStream_t st);
 
 // Decode attention over head-major fp16 caches [n_kv][max_ctx][hd], positions
-// 0..*pos_ptr: kAttnSplitLen-position splits, then a merge launch.  `part`
-// holds attn_decode_workspace() floats.  rope = true rotates q and the new k
-// at *pos_ptr and writes the new k/v rows (fp16) in the split launch.
-constexpr int kAttnSplitLen = 128;
+// 0..*pos_ptr: kAttnSplitLen-position splits, each walked in chunks of
+// kAttnRows rows per lane, then a merge launch (out != nullptr) or nothing (the
+// partials are left for a matvec with kPreAttnMerge).  `part` holds
+// attn_decode_workspace() floats: per head and split [m, l, -, -, acc[hd]]
+// (kAttnPartStride(hd) floats).  rope = true rotates q and the new k at
+// *pos_ptr and writes the new k/v rows (fp16) in the split launch.
+constexpr int kAttnSplitLen = 512;
+constexpr int kAttnRows = 4;
+constexpr int kAttnMaxSplits = 64;
+constexpr int kAttnMergeMaxSplits = 8;  // splits a matvec merges in its x prologue (max_ctx <= 4096)
+constexpr int kAttnPartStride(int hd) { return hd + 4; }
 int attn_decode_splits(int max_ctx);
 int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx);
 // rope_table (optional, with rope): [max_ctx][hd] floats from rope_table_launch,
@@ -123,6 +138,8 @@ int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx);
 int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* part, float* out, int n_heads,
                        int n_kv, int hd, const int* pos_ptr, int max_ctx, bool rope, float theta, hipStream_t st,
                        const float* rope_table = nullptr);
+// out[h][t] = the merge of the split partials `part` of head h (attn_decode_merge).
+int attn_merge_launch(const float* part, float* out, int n_heads, int hd, int max_ctx, hipStream_t st);
 // table[p][2i], table[p][2i + 1] = cos, sin of RoPE pair i at position p < max_ctx.
 int rope_table_launch(float* table, int hd, int max_ctx, float theta, hipStream_t st);
 

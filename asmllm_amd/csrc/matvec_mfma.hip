@@ -357,14 +357,19 @@ __device__ __forceinline__ float tile_total(float acc) {
 
 // PW > 0: every wave streams exactly PW units of each tile (K = 256 NW PW), so
 // its x operands are the same for every tile and stay in registers; PW = 0:
-// any K, operands read from LDS per unit.
-template <int QT, int XQ, int NW, int D, int PW>
+// any K, operands read from LDS per unit.  AMS > 0: x is the decode attention
+// output, merged in this launch from the AMS split states per head in pre_arg
+// (kPreAttnMerge: heads of pre_hd dimensions, pre_hd % 32 == 0, one x item per
+// thread); the states are requested before the weight stream, as x is, with a
+// fixed number of loads per wave so the wait for them does not also wait for
+// the weights.
+template <int QT, int XQ, int NW, int D, int PW, int AMS>
 __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __restrict__ w,
                                                             const uint8_t* __restrict__ wh,
                                                             const float* __restrict__ wsc,
                                                             const float* __restrict__ x, float* __restrict__ y,
                                                             int M, int K, int pre, const float* __restrict__ pre_arg,
-                                                            float eps, int accumulate, int post) {
+                                                            float eps, int accumulate, int post, int pre_hd) {
     using U = Unit<QT>;
     constexpr int kThreads = NW * 64;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -432,15 +437,28 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     // of one A-operand lane.
     const int ni = nb * 4;
     float4 xv[XQ][2], av[XQ][2];
+    constexpr bool AM = AMS > 0;
+    AttnMergeQuads<AM ? AMS : 1> am;
+    // waves holding x items (a wave-uniform test: in a wave past the last item
+    // no load is issued, in the others every lane loads)
+    const bool am_items = wave * 64 < ni;
+    if constexpr (AM) {
+        static_assert(XQ == 1, "the attention merge takes one x item per thread");
+        const int it = min((int)threadIdx.x, ni - 1);
+        const int off = 32 * (it >> 2) + 4 * (it & 3);  // positions off.. and off + 16.. of one head
+        const int hh = off / pre_hd;
+        if (am_items) am.load(pre_arg + (size_t)hh * AMS * (pre_hd + 4), pre_hd + 4, off - hh * pre_hd);
+    } else {
 #pragma unroll
-    for (int i = 0; i < XQ; ++i) {
-        const int it = min((int)threadIdx.x + kThreads * i, ni - 1);
-        const int off = 32 * (it >> 2) + 4 * (it & 3);
-        xv[i][0] = *reinterpret_cast<const float4*>(x + off);
-        xv[i][1] = *reinterpret_cast<const float4*>(x + off + 16);
-        if (pre != kPreNone) {
-            av[i][0] = *reinterpret_cast<const float4*>(pre_arg + off);
-            av[i][1] = *reinterpret_cast<const float4*>(pre_arg + off + 16);
+        for (int i = 0; i < XQ; ++i) {
+            const int it = min((int)threadIdx.x + kThreads * i, ni - 1);
+            const int off = 32 * (it >> 2) + 4 * (it & 3);
+            xv[i][0] = *reinterpret_cast<const float4*>(x + off);
+            xv[i][1] = *reinterpret_cast<const float4*>(x + off + 16);
+            if (pre != kPreNone) {
+                av[i][0] = *reinterpret_cast<const float4*>(pre_arg + off);
+                av[i][1] = *reinterpret_cast<const float4*>(pre_arg + off + 16);
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -453,7 +471,10 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
 
     // 3) fused pre-op on x, then digits; partial sums start at zero.
     for (int i = threadIdx.x; i < my_tiles * NW * 16; i += kThreads) part[i] = 0.f;
-    if (pre == kPreRmsNorm) {
+    if constexpr (AM) {
+        if (am_items) am.finish(&xv[0][0], &xv[0][1]);
+        else xv[0][0] = xv[0][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // no item: no digit writes below
+    } else if (pre == kPreRmsNorm) {
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < XQ; ++i)
@@ -665,14 +686,14 @@ struct Planes {
     const float* wsc;
 };
 
-template <int QT, int XQ, int NW, int D, int PW>
+template <int QT, int XQ, int NW, int D, int PW, int AMS = 0>
 int launch_xq(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
-    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW>;
+    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW, AMS>;
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
-    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW>), dim3(grid), dim3(NW * 64), lds, st, pw.w, pw.wh,
-                       pw.wsc, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate, o.post);
+    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS>), dim3(grid), dim3(NW * 64), lds, st, pw.w, pw.wh,
+                       pw.wsc, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate, o.post, o.attn_hd);
     return kOk;
 }
 
@@ -743,11 +764,35 @@ bool mfma_eligible(const Planes& pw, const float* x, const MatvecOpts& o, int64_
     const int64_t plane = (M + 16) * nb * U::kMainPerBlock;  // largest plane, with the last tile's padding
     bool aligned = (uintptr_t)pw.w % 4 == 0;
     if (U::kSplit) aligned = (uintptr_t)pw.w % 16 == 0 && (uintptr_t)pw.wsc % 16 == 0 && (!U::kQ5 || (uintptr_t)pw.wh % 16 == 0);
+    if (o.pre == kPreAttnMerge) {  // one x item per thread of the 16-wave shape, heads of whole 32-blocks
+        const StreamShape sh = stream_shape(U::kSlotBytes, M, K);
+        if (QT != kFmtQ4_0 || o.post != kPostNone || sh.waves != kWideWaves || nb * 4 > kWideWaves * 64 ||
+            o.attn_hd <= 0 || o.attn_hd % 32 || K % o.attn_hd || o.attn_splits < 1 ||
+            o.attn_splits > kAttnMergeMaxSplits)
+            return false;
+    }
     return K % 256 == 0 && nb >= kUnitBlocks && nb <= kMaxBlocks && M >= 1 && M <= INT32_MAX - 16 &&
            plane < (int64_t)kPastEnd && aligned && (uintptr_t)x % 16 == 0 &&
            (o.pre == kPreNone || (uintptr_t)o.pre_arg % 16 == 0) &&
            (o.post == kPostNone || (M % 16 == 0 && !o.accumulate && !U::kSplit)) &&
            stream_shape(U::kSlotBytes, M, K).lds <= kLdsBudget;
+}
+
+// The attention-merge stream for the split count of the launch (1..kAttnMergeMaxSplits).
+template <int QT, int PW>
+int launch_merge(const Planes& pw, const float* x, float* y, int m, int k, const StreamShape& sh, hipStream_t st,
+                 const MatvecOpts& o) {
+    switch (o.attn_splits) {
+        case 1: return launch_xq<QT, 1, kWideWaves, kWideDepth, PW, 1>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        case 2: return launch_xq<QT, 1, kWideWaves, kWideDepth, PW, 2>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        case 3: return launch_xq<QT, 1, kWideWaves, kWideDepth, PW, 3>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        case 4: return launch_xq<QT, 1, kWideWaves, kWideDepth, PW, 4>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        case 5: return launch_xq<QT, 1, kWideWaves, kWideDepth, PW, 5>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        case 6: return launch_xq<QT, 1, kWideWaves, kWideDepth, PW, 6>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        case 7: return launch_xq<QT, 1, kWideWaves, kWideDepth, PW, 7>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        case 8: return launch_xq<QT, 1, kWideWaves, kWideDepth, PW, 8>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        default: return fail(kUnsupported, "attention merge stream: %d splits", o.attn_splits);
+    }
 }
 
 template <int QT>
@@ -757,6 +802,15 @@ int mfma_launch(const Planes& pw, const float* x, float* y, int64_t M, int64_t K
     const StreamShape sh = stream_shape(Unit<QT>::kSlotBytes, M, K);
     const int m = (int)M, k = (int)K;
     int rc;
+    if constexpr (QT == kFmtQ4_0) {
+        if (o.pre == kPreAttnMerge) {  // eligibility fixed the 16-wave shape with one x item per thread
+            rc = nb / kUnitBlocks == kWideWaves ? launch_merge<QT, 1>(pw, x, y, m, k, sh, st, o)
+                                                : launch_merge<QT, 0>(pw, x, y, m, k, sh, st, o);
+            if (rc) return rc;
+            ASMHIP_TRY(hipGetLastError());
+            return kOk;
+        }
+    }
     if (sh.waves == kWideWaves && nb / kUnitBlocks == kWideWaves)
         // K = 4096: one unit per wave and tile, the wave's x operands in registers
         rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1>(pw, x, y, m, k, sh.grid, sh.lds, st, o);

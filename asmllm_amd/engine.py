@@ -20,8 +20,11 @@ stream, so it can be captured once into a HIP graph and replayed per token:
     the argmax kernel writes the next token and advances the position, so a
     replayed graph walks the sequence without host involvement;
   * RoPE and the KV-cache write are fused into the attention launch
-    (asmhip_attention_decode_rope_table), its cos/sin read from a table of
-    every position's angles formed once at set-up (asmhip_rope_table);
+    (asmhip_attention_decode_partials_rope_table), its cos/sin read from a
+    table of every position's angles formed once at set-up
+    (asmhip_rope_table); the attention leaves its 512-position splits'
+    softmax states in a workspace, and the o matvec merges them as it reads
+    its x (asmhip_matmul_attn_output), so attention + o take two launches;
   * the KV cache is fp16, head-major [n_kv_heads][max_ctx][head_dim] per layer
     (the reference keeps fp32 [128][heads][head_dim], generate.py:252-253);
   * head_dim 48 (the reference's stories15M demo model, dim 288), 64 or 128;
@@ -338,11 +341,12 @@ class DecodeEngine:
         check(embed(self.embed.ptr, self.token.ptr, self.x.ptr, s.vocab, d, st), "embed")
         for ly in self.layers:
             normed(ly.attn_norm, s.qkv_rows, ly.wqkv, self.qkv.ptr, "qkv matvec")
-            check(L.asmhip_attention_decode_rope_table(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr,
-                                                       self.workspace.ptr, self.attn.ptr, s.n_heads, s.n_kv_heads, hd,
-                                                       self.pos.ptr, self.max_ctx, self.rope_table.ptr, st),
+            check(L.asmhip_attention_decode_partials_rope_table(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr,
+                                                                self.workspace.ptr, s.n_heads, s.n_kv_heads, hd,
+                                                                self.pos.ptr, self.max_ctx, self.rope_table.ptr, st),
                   "rope + attention")
-            mv(ly.wo, self.attn.ptr, self.x.ptr, d, d, NONE, None, 1, "o matvec")
+            check(L.asmhip_matmul_attn_output(Q4, ly.wo.ptr, self.workspace.ptr, self.attn.ptr, self.x.ptr, d,
+                                              s.n_heads, hd, self.max_ctx, 1, st), "merge + o matvec")
             xin, pre, arg = norm_in(ly.ffn_norm)
             check(L.asmhip_matmul_swiglu(Q4, ly.wgu.ptr, xin, self.ffn.ptr, h, d, pre, arg, eps, self.gu.ptr, st),
                   "gate/up matvec + swiglu")

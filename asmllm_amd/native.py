@@ -75,6 +75,8 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_attention_decode_rope": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, c_float, _P]),
     "asmhip_rope_table": (c_int, [_P, c_int, c_int, c_float, _P]),
     "asmhip_attention_decode_rope_table": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, _P, _P]),
+    "asmhip_attention_decode_partials_rope_table": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, _P, _P]),
+    "asmhip_matmul_attn_output": (c_int, [c_int, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, _P]),
     "asmhip_stream_read": (c_int, [_P, c_int64, _P, _P]),
     "asmhip_attention_decode_noalloc_max_floats": (c_int64, []),
     "asmhip_attention_decode_rope_noalloc": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, c_float, _P]),

@@ -212,7 +212,7 @@ ASMHIP_API int asmhip_attention(const float* q, const float* k, const float* v, 
  * place and writes rotated k and v at position *pos_dev.
  * asmhip_attention_decode computes, per head h (kv head h / (n_heads /
  * n_kv_heads)), softmax(q_h . k_p / sqrt(head_dim)) . v_p over positions
- * 0..*pos_dev (max_ctx <= 8192); workspace holds
+ * 0..*pos_dev (max_ctx <= 32768); workspace holds
  * asmhip_attention_decode_workspace() floats (calls sharing one workspace
  * must not overlap).  head_dim 48, 64 or 128. */
 ASMHIP_API int asmhip_rope_kv_write(float* qkv, void* k_cache, void* v_cache, int n_heads, int n_kv_heads,
@@ -239,6 +239,27 @@ ASMHIP_API int asmhip_attention_decode_rope_table(const float* qkv, void* k_cach
                                                   float* out, int n_heads, int n_kv_heads, int head_dim,
                                                   const int* pos_dev, int max_ctx, const float* rope_table,
                                                   void* stream);
+/* The decode step's attention and o projection in two launches instead of
+ * three (generate.py:283-300: per-head softmax(q k^T) v, then the o matvec and
+ * the residual add).  asmhip_attention_decode_partials_rope_table is
+ * asmhip_attention_decode_rope_table without its merge launch: it leaves every
+ * 512-position split's softmax state in `workspace`
+ * (asmhip_attention_decode_workspace() floats, 16-byte aligned).
+ * asmhip_matmul_attn_output then computes y = W . attn (accumulate: y += W .
+ * attn) for GGUF blocks W [M][n_heads * head_dim / 32] (qtype Q4_0 or Q8_0),
+ * where attn is the merged attention output: for Q4_0 where the int8-MFMA
+ * stream takes the shape (head_dim 64 or 128, n_heads * head_dim a multiple of
+ * 256 and at most 8192, max_ctx <= 4096) the merge runs inside the matvec's
+ * read of x; otherwise a merge launch writes attn to `work` (n_heads *
+ * head_dim floats) and a matvec reads it.  Results equal the merge launch + asmhip_matmul_fused, bit for bit.
+ * `workspace` and `max_ctx` must be those of the attention call. */
+ASMHIP_API int asmhip_attention_decode_partials_rope_table(const float* qkv, void* k_cache, void* v_cache,
+                                                           float* workspace, int n_heads, int n_kv_heads,
+                                                           int head_dim, const int* pos_dev, int max_ctx,
+                                                           const float* rope_table, void* stream);
+ASMHIP_API int asmhip_matmul_attn_output(int qtype, const void* blocks, const float* workspace, float* work, float* y,
+                                         int64_t M, int n_heads, int head_dim, int max_ctx, int accumulate,
+                                         void* stream);
 /* Measurement, not part of the path: reads `bytes` (< 2 GiB) of device memory
  * in one launch, every workgroup one contiguous chunk with all loads issued up
  * front, and keeps nothing; `sink` is 4 KB of device memory.  Its time is the
@@ -250,7 +271,7 @@ ASMHIP_API int asmhip_stream_read(const void* buf, int64_t bytes, void* sink, vo
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
  * split partials go to a fixed per-device scratch array of
  * asmhip_attention_decode_noalloc_max_floats() floats (4 MiB); shapes needing
- * more (n_heads * ceil(max_ctx / 128) * (head_dim + 2) floats) are rejected with
+ * more (n_heads * ceil(max_ctx / 512) * (head_dim + 4) floats) are rejected with
  * ASMHIP_ERR_INVALID_ARGUMENT.  Calls that overlap on one GPU share the array and
  * race; nothing in it needs clearing between calls.  Same results, bit for bit,
  * as asmhip_attention_decode_rope. */

@@ -136,6 +136,10 @@ def _random_attention_cases(n, seed):
     (32, 8, 128, 128, 300), (4, 4, 128, 127, 128), (8, 8, 64, 8191, 8192),
     # head_dim 48 (stories15M): one split, several, and 64 splits (more than the merge's 48 threads)
     (6, 6, 48, 5, 64), (6, 6, 48, 300, 2048), (6, 2, 48, 8000, 8192),
+    # split (512 positions) and chunk (64 / 128 positions) boundaries, a split
+    # holding only pos, and a cache of 64 splits (the most the merge takes)
+    (4, 4, 128, 511, 600), (4, 2, 128, 512, 600), (4, 4, 128, 513, 1100), (4, 4, 128, 63, 64),
+    (4, 4, 128, 64, 130), (8, 4, 64, 127, 1024), (6, 6, 48, 1535, 1537), (2, 1, 128, 32767, 32768),
 ] + _random_attention_cases(8, 77))
 def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos, max_ctx):
     rng = np.random.default_rng(n_heads * 1000 + pos)
@@ -358,3 +362,69 @@ def test_argmax_non_finite_as_numpy(hip, n, case):
     _ok(hip, hip.asmhip_argmax(dl.ptr, n, dtok.ptr, None, None))
     synchronize()
     assert int(dtok.download(np.int32, 1)[0]) == int(np.argmax(logits))
+
+
+@pytest.mark.parametrize("qtype", [native.Q4_0, native.Q8_0])
+@pytest.mark.parametrize("n_heads,n_kv,hd,pos,max_ctx,M", [
+    (32, 32, 128, 2048, 2176, 4096),   # the 7B step: the merge inside the int8-MFMA matvec
+    (8, 2, 64, 300, 1024, 384),        # K = 512: the MFMA stream with its x from LDS
+    (16, 4, 128, 5000, 6000, 200),     # 12 splits: more than are requested up front
+    (16, 16, 64, 0, 100, 32),          # one position, one split
+    (6, 6, 48, 100, 256, 288),         # K = 288 (stories15M): merge launch + matvec
+])
+def test_attention_partials_and_fused_attn_output(hip, qtype, n_heads, n_kv, hd, pos, max_ctx, M):
+    """asmhip_attention_decode_partials_rope_table + asmhip_matmul_attn_output (the
+    merge of the split states inside the o matvec's read of x) equal, bit for bit,
+    asmhip_attention_decode_rope_table (split launch + merge launch) followed by
+    asmhip_matmul_fused on its output, accumulating and overwriting; the caches
+    written the same way."""
+    K = n_heads * hd
+    rng = np.random.default_rng(pos + M)
+    qkv = rng.standard_normal((n_heads + 2 * n_kv) * hd).astype(np.float32)
+    kc = np.zeros((n_kv, max_ctx, hd), np.float16)
+    vc = np.zeros((n_kv, max_ctx, hd), np.float16)
+    kc[:, :pos] = rng.standard_normal((n_kv, pos, hd))
+    vc[:, :pos] = rng.standard_normal((n_kv, pos, hd))
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    blocks = gguf.quantize_q4_0(w) if qtype == native.Q4_0 else gguf.quantize_q8_0(w)
+    y0 = rng.standard_normal(M).astype(np.float32)
+    db, dpos = DeviceBuffer.from_numpy(blocks), DeviceBuffer.from_numpy(np.array([pos], np.int32))
+    table = DeviceBuffer(max_ctx * hd * 4)
+    _ok(hip, hip.asmhip_rope_table(table.ptr, hd, max_ctx, 10000.0, None))
+    ws_n = hip.asmhip_attention_decode_workspace(n_heads, hd, max_ctx)
+    outs = {}
+    for fused in (False, True):
+        dqkv, dkc, dvc = DeviceBuffer.from_numpy(qkv), DeviceBuffer.from_numpy(kc), DeviceBuffer.from_numpy(vc)
+        dws, dattn = DeviceBuffer(ws_n * 4), DeviceBuffer(K * 4)
+        ya, yo = DeviceBuffer.from_numpy(y0), DeviceBuffer(M * 4)
+        if fused:
+            _ok(hip, hip.asmhip_attention_decode_partials_rope_table(dqkv.ptr, dkc.ptr, dvc.ptr, dws.ptr, n_heads,
+                                                                     n_kv, hd, dpos.ptr, max_ctx, table.ptr, None))
+            for y, acc in ((ya, 1), (yo, 0)):
+                _ok(hip, hip.asmhip_matmul_attn_output(qtype, db.ptr, dws.ptr, dattn.ptr, y.ptr, M, n_heads, hd,
+                                                       max_ctx, acc, None))
+        else:
+            _ok(hip, hip.asmhip_attention_decode_rope_table(dqkv.ptr, dkc.ptr, dvc.ptr, dws.ptr, dattn.ptr, n_heads,
+                                                            n_kv, hd, dpos.ptr, max_ctx, table.ptr, None))
+            for y, acc in ((ya, 1), (yo, 0)):
+                _ok(hip, hip.asmhip_matmul_fused(qtype, db.ptr, dattn.ptr, y.ptr, M, K, native.PRE_NONE, None,
+                                                 0.0, acc, None))
+        synchronize()
+        outs[fused] = (ya.download(np.float32, M), yo.download(np.float32, M),
+                       dkc.download(np.float16, kc.shape), dvc.download(np.float16, vc.shape))
+    for a, b in zip(outs[True], outs[False]):
+        np.testing.assert_array_equal(a.view(np.uint16 if a.dtype == np.float16 else np.uint32),
+                                      b.view(np.uint16 if b.dtype == np.float16 else np.uint32))
+    assert np.all(np.isfinite(outs[True][0]))
+    # and the values themselves: y0 + W attn against the oracle's fp16-cache attention
+    from oracle import native as oracle
+    q = qkv[: n_heads * hd].reshape(n_heads, hd)
+    k = qkv[n_heads * hd: (n_heads + n_kv) * hd].reshape(n_kv, hd)
+    q_rot = np.stack([oracle.rope(q[h], k[0], hd, pos, 10000.0)[0] for h in range(n_heads)])
+    kc_o = np.ascontiguousarray(outs[True][2].transpose(1, 0, 2)).view(np.uint16)
+    vc_o = np.ascontiguousarray(outs[True][3].transpose(1, 0, 2)).view(np.uint16)
+    attn = oracle.attention_decode_f16(q_rot, kc_o, vc_o, pos + 1, n_kv, 8).reshape(K).astype(np.float32)
+    wq = gguf.dequantize_q4_0(blocks) if qtype == native.Q4_0 else gguf.dequantize_q8_0(blocks)
+    ref = wq.astype(np.float64) @ attn.astype(np.float64)
+    l1 = np.abs(wq.astype(np.float64)) @ np.abs(attn.astype(np.float64))
+    assert np.all(np.abs(outs[True][1] - ref) <= 1e-4 * l1 + 1e-6)

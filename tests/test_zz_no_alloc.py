@@ -56,7 +56,7 @@ def test_noalloc_matches_workspace_entry_point_twice(hip):
 def test_noalloc_rejects_shapes_beyond_its_scratch(hip):
     cap = hip.asmhip_attention_decode_noalloc_max_floats()
     assert cap == 1 << 20
-    # 512 heads x 64 splits x 130 floats > 2^20
+    # 512 heads x 16 splits x 132 floats > 2^20
     assert hip.asmhip_attention_decode_rope_noalloc(1, 1, 1, 1, 512, 512, 128, 1, 8192, 10000.0, None) == \
         native.ERR_INVALID_ARGUMENT
     assert "scratch" in hip.asmhip_last_error().decode()
