@@ -363,7 +363,7 @@ __device__ __forceinline__ float tile_total(float acc) {
 // thread); the states are requested before the weight stream, as x is, with a
 // fixed number of loads per wave so the wait for them does not also wait for
 // the weights.
-template <int QT, int XQ, int NW, int D, int PW, int AMS>
+template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW>
 __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __restrict__ w,
                                                             const uint8_t* __restrict__ wh,
                                                             const float* __restrict__ wsc,
@@ -418,7 +418,8 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
 #pragma unroll
         for (int k = 0; k < U::kLoads; ++k) {
             if (!U::kSplit || 64 * k + 63 < U::kMainPieces) {  // the whole load is main plane
-                buf[k] = buf_load_b128(wr, s < L ? base + poff[k] : kPastEnd);
+                buf[k] = NTW ? buf_load_b128_nt(wr, s < L ? base + poff[k] : kPastEnd)
+                             : buf_load_b128(wr, s < L ? base + poff[k] : kPastEnd);
             } else {  // split tail: qh (Q5, lanes 0-31) and scale slices; no piece for the rest
                 const int q = lane + 64 * k - U::kMainPieces;
                 const uint32_t o = s < L ? base4 + poff[k] : kPastEnd;
@@ -516,6 +517,9 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     }
 #pragma unroll
     for (int i = 0; i < XQ; ++i) {
+        // a wave whose items of this round are all past the last one skips the
+        // round (wave-uniform), leaving its SIMD to the waves that have items
+        if (i > 0 && kThreads * i + 64 * wave >= ni) break;
         const int it = (int)threadIdx.x + kThreads * i;
         const float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
                             xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
@@ -686,13 +690,13 @@ struct Planes {
     const float* wsc;
 };
 
-template <int QT, int XQ, int NW, int D, int PW, int AMS = 0>
+template <int QT, int XQ, int NW, int D, int PW, int AMS = 0, bool NTW = false>
 int launch_xq(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
-    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW, AMS>;
+    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW>;
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
-    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS>), dim3(grid), dim3(NW * 64), lds, st, pw.w, pw.wh,
+    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW>), dim3(grid), dim3(NW * 64), lds, st, pw.w, pw.wh,
                        pw.wsc, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate, o.post, o.attn_hd);
     return kOk;
 }
@@ -811,10 +815,17 @@ int mfma_launch(const Planes& pw, const float* x, float* y, int64_t M, int64_t K
             return kOk;
         }
     }
-    if (sh.waves == kWideWaves && nb / kUnitBlocks == kWideWaves)
-        // K = 4096: one unit per wave and tile, the wave's x operands in registers
-        rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
-    else if (sh.waves == kWideWaves)
+    if (sh.waves == kWideWaves && nb / kUnitBlocks == kWideWaves) {
+        // K = 4096: one unit per wave and tile, the wave's x operands in registers;
+        // Q4_0 with at most 128 tiles (M <= 2048) reads its weights with nontemporal
+        // loads (measured: 1024x4096 4.29 -> 3.95 us; no gain from 4096 rows up)
+        rc = -1;
+        if constexpr (QT == kFmtQ4_0) {
+            if ((M + 15) / 16 <= 128)
+                rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1, 0, true>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        }
+        if (rc == -1) rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+    } else if (sh.waves == kWideWaves)
         rc = launch_nw<QT, kWideWaves, kWideDepth>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
     else
         rc = launch_nw<QT, kNarrowWaves, kNarrowDepth>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
