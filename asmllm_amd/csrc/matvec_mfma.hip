@@ -820,12 +820,11 @@ int mfma_launch(const Planes& pw, const float* x, float* y, int64_t M, int64_t K
         // nontemporal weight loads for Q4_0 with at most 128 tiles (M <= 2048;
         // measured: 1024x4096 4.29 -> 3.95 us, no gain from 4096 rows up) and for
         // Q8_0 (4096x4096 6.37 -> 6.18 us, 11008x4096 11.3 -> 11.0 us)
-        rc = -1;
-        if constexpr (QT == kFmtQ4_0 || QT == kFmtQ8_0) {
-            if (QT == kFmtQ8_0 || (M + 15) / 16 <= 128)
-                rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1, 0, true>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
-        }
-        if (rc == -1) rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        constexpr bool kNtFormat = QT == kFmtQ4_0 || QT == kFmtQ8_0;
+        if (kNtFormat && (QT == kFmtQ8_0 || (M + 15) / 16 <= 128))
+            rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1, 0, kNtFormat>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
+        else
+            rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
     } else if (sh.waves == kWideWaves)
         rc = launch_nw<QT, kWideWaves, kWideDepth>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
     else
