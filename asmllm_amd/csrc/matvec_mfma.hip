@@ -363,7 +363,7 @@ __device__ __forceinline__ float tile_total(float acc) {
 // thread); the states are requested before the weight stream, as x is, with a
 // fixed number of loads per wave so the wait for them does not also wait for
 // the weights.
-template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW>
+template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH>
 __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __restrict__ w,
                                                             const uint8_t* __restrict__ wh,
                                                             const float* __restrict__ wsc,
@@ -381,7 +381,10 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     const uint32_t row_bytes4 = (uint32_t)nb * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int G = gridDim.x;
-    const int n_tiles = (M + 15) >> 4;
+    // tiles of TH rows (16, or 8 for small Q8_0 matvecs); MFMA rows TH..15 of
+    // a tile load zeros
+    static_assert(TH == 16 || TH == 8, "tile height");
+    const int n_tiles = (M + TH - 1) >> (TH == 16 ? 4 : 3);
     const int my_tiles = (n_tiles - (int)blockIdx.x + G - 1) / G;
     const int per_w = wave < nu ? (nu - wave + NW - 1) / NW : 0;  // this wave's units per tile
     const int L = my_tiles * per_w;                              // length of this wave's stream
@@ -395,34 +398,38 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
 
     // This lane's 16-byte pieces of a unit: piece q = lane + 64 k (see piece_lds).
     // Main-plane pieces past the unit (GGUF tails) are clamped to its last piece
-    // and not parked; rows past M fall beyond the buffer and load zeros.
+    // and not parked; rows past M fall beyond the buffer and load zeros, and so
+    // do the pieces of rows TH..15 (plive false).
     uint32_t poff[U::kLoads];
+    bool plive[U::kLoads];
 #pragma unroll
     for (int k = 0; k < U::kLoads; ++k) {
         const int q = lane + 64 * k;
         if (!U::kSplit || q < U::kMainPieces) {
             const int qc = min(q, U::kMainPieces - 1);
             poff[k] = (uint32_t)(qc / U::kCols) * row_bytes + 16u * (uint32_t)(qc % U::kCols);
+            plive[k] = TH == 16 || qc / U::kCols < TH;
         } else {
             const int i = (q - U::kMainPieces) & 31;  // row i / 2, half i % 2 of a qh or scale slice
             poff[k] = (uint32_t)(i >> 1) * row_bytes4 + 16u * (uint32_t)(i & 1);
+            plive[k] = TH == 16 || (i >> 1) < TH;
         }
     }
     // unit s of the stream -> (tile slot i, unit u)
     auto load_unit = [&](uint4* buf, int s) {
         const int i = s / max(per_w, 1);
         const int u = wave + NW * (s - i * per_w);
-        const uint32_t row0 = (uint32_t)(((int)blockIdx.x + G * i) * 16);
+        const uint32_t row0 = (uint32_t)(((int)blockIdx.x + G * i) * TH);
         const uint32_t base = s < L ? row0 * row_bytes + (uint32_t)u * (uint32_t)U::kMainRow : kPastEnd;
         const uint32_t base4 = s < L ? row0 * row_bytes4 + (uint32_t)u * 32u : kPastEnd;
 #pragma unroll
         for (int k = 0; k < U::kLoads; ++k) {
             if (!U::kSplit || 64 * k + 63 < U::kMainPieces) {  // the whole load is main plane
-                buf[k] = NTW ? buf_load_b128_nt(wr, s < L ? base + poff[k] : kPastEnd)
-                             : buf_load_b128(wr, s < L ? base + poff[k] : kPastEnd);
+                const uint32_t o = s < L && plive[k] ? base + poff[k] : kPastEnd;
+                buf[k] = NTW ? buf_load_b128_nt(wr, o) : buf_load_b128(wr, o);
             } else {  // split tail: qh (Q5, lanes 0-31) and scale slices; no piece for the rest
                 const int q = lane + 64 * k - U::kMainPieces;
-                const uint32_t o = s < L ? base4 + poff[k] : kPastEnd;
+                const uint32_t o = s < L && plive[k] ? base4 + poff[k] : kPastEnd;
                 if (U::kQ5 && q < 32)
                     buf[k] = buf_load_b128(hr, o);
                 else if (q < (U::kQ5 ? 64 : 32))
@@ -646,7 +653,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
 
     // 5) add the waves' partial sums of every row in a fixed order.
     if (post == kPostSwiGlu8) {
-        // a tile is 8 gate rows and their 8 up rows (M % 16 == 0): y[8 tile + r] = silu(gate) * up
+        // a tile is 8 gate rows and their 8 up rows (M % 16 == 0, TH = 16): y[8 tile + r] = silu(gate) * up
         for (int idx = threadIdx.x; idx < my_tiles * 8; idx += kThreads) {
             const int i = idx >> 3, r = idx & 7;
             const int tile = (int)blockIdx.x + G * i;
@@ -662,8 +669,8 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     }
     for (int idx = threadIdx.x; idx < my_tiles * 16; idx += kThreads) {
         const int i = idx >> 4, r = idx & 15;
-        const int row = ((int)blockIdx.x + G * i) * 16 + r;
-        if (row < M) {
+        const int row = ((int)blockIdx.x + G * i) * TH + r;
+        if (r < TH && row < M) {
             float sum = 0.f;
 #pragma unroll
             for (int k = 0; k < NW; ++k) sum += part[(i * NW + k) * 16 + r];
@@ -690,14 +697,14 @@ struct Planes {
     const float* wsc;
 };
 
-template <int QT, int XQ, int NW, int D, int PW, int AMS = 0, bool NTW = false>
+template <int QT, int XQ, int NW, int D, int PW, int AMS = 0, bool NTW = false, int TH = 16>
 int launch_xq(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
-    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW>;
+    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH>;
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
-    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW>), dim3(grid), dim3(NW * 64), lds, st, pw.w, pw.wh,
-                       pw.wsc, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate, o.post, o.attn_hd);
+    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH>), dim3(grid), dim3(NW * 64), lds, st, pw.w,
+                       pw.wh, pw.wsc, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate, o.post, o.attn_hd);
     return kOk;
 }
 
@@ -728,11 +735,13 @@ size_t stream_lds(int slot_bytes, int nw, int nb, int tiles_per_group) {
     return (size_t)nw * slot_bytes + (size_t)nb * (kXStride + 4) + (size_t)tiles_per_group * nw * 16 * sizeof(float);
 }
 
-StreamShape stream_shape(int slot_bytes, int64_t M, int64_t K) {
+// Workgroup layout for tiles of th rows (16; 8 for the small Q8_0 matvecs, see mfma_launch).
+StreamShape stream_shape(int slot_bytes, int64_t M, int64_t K, int th = 16) {
     const int nb = (int)(K / 32);
-    const int n_tiles = (int)((M + 15) / 16);
+    const int cus = compute_units();
     StreamShape sh;
-    sh.grid = std::max(std::min(n_tiles, compute_units()), (n_tiles + kMaxTilesPerGroup - 1) / kMaxTilesPerGroup);
+    const int n_tiles = (int)((M + th - 1) / th);
+    sh.grid = std::max(std::min(n_tiles, cus), (n_tiles + kMaxTilesPerGroup - 1) / kMaxTilesPerGroup);
     sh.tiles_per_group = (n_tiles + sh.grid - 1) / sh.grid;
     sh.waves = kWideWaves;
     sh.lds = stream_lds(slot_bytes, kWideWaves, nb, sh.tiles_per_group);
@@ -821,6 +830,24 @@ int mfma_launch(const Planes& pw, const float* x, float* y, int64_t M, int64_t K
         // measured: 1024x4096 4.29 -> 3.95 us, no gain from 4096 rows up) and for
         // Q8_0 (4096x4096 6.37 -> 6.18 us, 11008x4096 11.3 -> 11.0 us)
         constexpr bool kNtFormat = QT == kFmtQ4_0 || QT == kFmtQ8_0;
+        // Q8_0 and the split layouts with at most one 8-row tile per CU (M <= 2048
+        // on 256 CUs) run 8-row tiles: twice the workgroups, half the bytes each
+        // (measured at 32 / 1024 / 2048 rows: Q8_0 4.82 -> 4.32, 5.23 -> 4.79,
+        // 5.54 -> 5.22 us; Q8 split 4.86 -> 4.57, 5.35 -> 4.96, 5.94 -> 5.66;
+        // Q4 / Q5 split 0.05-0.15 us less).  GGUF Q4_0 and Q5_0 lost 0.05-0.2 us
+        // at 8 rows, and 4- to 1-row tiles lost for every format.
+        constexpr bool kEightRowFormat =
+            QT == kFmtQ8_0 || QT == kFmtQ8Split || QT == kFmtQ5Split || QT == kFmtQ4Split;
+        if constexpr (kEightRowFormat) {
+            const StreamShape s8 = stream_shape(Unit<QT>::kSlotBytes, M, K, 8);
+            if (o.post == kPostNone && (M + 7) / 8 <= compute_units() && s8.waves == kWideWaves) {
+                rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1, 0, kNtFormat, 8>(pw, x, y, m, k, s8.grid, s8.lds, st,
+                                                                                  o);
+                if (rc) return rc;
+                ASMHIP_TRY(hipGetLastError());
+                return kOk;
+            }
+        }
         if (kNtFormat && (QT == kFmtQ8_0 || (M + 15) / 16 <= 128))
             rc = launch_xq<QT, 1, kWideWaves, kWideDepth, 1, 0, kNtFormat>(pw, x, y, m, k, sh.grid, sh.lds, st, o);
         else

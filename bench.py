@@ -353,13 +353,25 @@ MATVEC_TABLE = [
     ("q4 split 11008x4096", "q4s", 11008, 4096),
     ("q5_0 11008x4096", "q5", 11008, 4096),
     ("q5 split 11008x4096", "q5s", 11008, 4096),
+    # the reference's quant-format sweep (bench/harness/bench_quant_formats.py:41-138):
+    # split-layout Q4/Q8/Q5 at M = 32 and 1024, K = 4096; GGUF Q4_0/Q8_0 beside them
+    ("formats q4 split 32x4096", "q4s", 32, 4096),
+    ("formats q8 split 32x4096", "q8s", 32, 4096),
+    ("formats q5 split 32x4096", "q5s", 32, 4096),
+    ("formats q4_0 32x4096", "q4", 32, 4096),
+    ("formats q8_0 32x4096", "q8", 32, 4096),
+    ("formats q4 split 1024x4096", "q4s", 1024, 4096),
+    ("formats q8 split 1024x4096", "q8s", 1024, 4096),
+    ("formats q5 split 1024x4096", "q5s", 1024, 4096),
+    ("formats q8_0 1024x4096", "q8", 1024, 4096),
 ]
 
 
-def _rotating_q5(M: int, K: int, copies: int, seed: int, split: bool, q4: bool = False):
+def _rotating_q5(M: int, K: int, copies: int, seed: int, split: bool, q4: bool = False, q8: bool = False):
     """`copies` device copies of one synthetic Q5_0 matrix (random nibbles and
     fifth bits, fp16 scales of N(0, 0.02^2) weights' size): GGUF blocks, or
-    the split ql / qh / fp32 scales planes (q4: the Q4 split qs / scales planes)."""
+    the split ql / qh / fp32 scales planes (q4: the Q4 split qs / scales planes;
+    q8: the Q8 split int8 qs / scales planes)."""
     from asmllm_amd import gguf
     from asmllm_amd.device import DeviceBuffer
 
@@ -368,7 +380,9 @@ def _rotating_q5(M: int, K: int, copies: int, seed: int, split: bool, q4: bool =
     ql = rng.integers(0, 256, (M, nb, 16), dtype=np.uint8)
     qh = rng.integers(0, 256, (M, nb, 4), dtype=np.uint8)
     d = (rng.uniform(0.001, 0.004, (M, nb)) * rng.choice([-1.0, 1.0], (M, nb))).astype(np.float16)
-    if q4:
+    if q8:
+        planes = (rng.integers(-127, 128, (M, nb, 32), dtype=np.int8), d.astype(np.float32))
+    elif q4:
         planes = (ql, d.astype(np.float32))
     else:
         planes = (ql, qh, d.astype(np.float32)) if split else (gguf.pack_q5_0(ql, qh, d),)
@@ -393,16 +407,18 @@ def bench_matvec_table(min_rotated_bytes: int = 600_000_000) -> list[dict]:
     lib = native.lib()
     rows = []
     for name, qt, M, K in MATVEC_TABLE:
-        blk = {"q4": 18, "q8": 34, "q5": 22, "q5s": 24, "q4s": 20}[qt]
+        blk = {"q4": 18, "q8": 34, "q5": 22, "q5s": 24, "q4s": 20, "q8s": 36}[qt]
         copies = max(8, -(-min_rotated_bytes // (M * (K // 32) * blk)))
         dx, dy = DeviceBuffer(4 * K), DeviceBuffer(4 * M)
         native.check(lib.asmhip_fill_f32(dx.ptr, K, 0.5, None), "fill")
-        if qt in ("q5", "q5s", "q4s"):
-            sets, _ = _rotating_q5(M, K, copies, seed=M * 7 + K, split=qt != "q5", q4=qt == "q4s")
-            if qt == "q4s":
-                def enqueue(i, st, sets=sets, dx=dx, dy=dy, M=M, K=K, name=name):
+        if qt in ("q5", "q5s", "q4s", "q8s"):
+            sets, _ = _rotating_q5(M, K, copies, seed=M * 7 + K, split=qt != "q5", q4=qt == "q4s", q8=qt == "q8s")
+            if qt in ("q4s", "q8s"):
+                fn = lib.asmhip_matmul_q4_split if qt == "q4s" else lib.asmhip_matmul_q8_split
+
+                def enqueue(i, st, sets=sets, dx=dx, dy=dy, M=M, K=K, name=name, fn=fn):
                     qs, sc = sets[i % len(sets)]
-                    native.check(lib.asmhip_matmul_q4_split(qs.ptr, sc.ptr, dx.ptr, dy.ptr, M, K, st), name)
+                    native.check(fn(qs.ptr, sc.ptr, dx.ptr, dy.ptr, M, K, st), name)
             elif qt == "q5":
                 def enqueue(i, st, sets=sets, dx=dx, dy=dy, M=M, K=K, name=name):
                     w = sets[i % len(sets)]

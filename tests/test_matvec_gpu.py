@@ -310,6 +310,48 @@ def test_q8_gguf_and_split_both_kernels(hip, oracle, q4_kernel, M, K):
         assert_matvec_close(dy.download(np.float32, M), ref, w, x)
 
 
+TILE_HEIGHT_ROWS = [1, 2, 3, 5, 16, 17, 31, 64, 100, 255, 256, 513, 1000, 1024, 2047, 2048, 4095]
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q8", "q4s", "q8s"])
+@pytest.mark.parametrize("K", [2048, 4096, 11008])
+def test_rows_do_not_depend_on_tile_height(hip, oracle, fmt, K):
+    """Below one 16-row tile per compute unit the MFMA stream cuts the rows into
+    tiles of 8, 4, 2 or 1 rows (at most one per CU), so a small matvec spreads its
+    bytes over the chip.  A row's value must not depend on the tile height: the
+    leading m rows of a 4096-row matrix (16-row tiles) give bitwise its first m
+    outputs, for every m from 1 row (1-row tiles) up; the whole matrix stays within
+    the bar of the oracle."""
+    M = 4096
+    blocks, x = _weights(K + len(fmt), M, K, qt=fmt[:2])
+    split = fmt.endswith("s")
+    if fmt == "q4s":
+        planes, fn = gguf.split_q4_0(blocks), hip.asmhip_matmul_q4_split
+    elif fmt == "q8s":
+        planes, fn = gguf.split_q8_0(blocks), hip.asmhip_matmul_q8_split
+    else:
+        planes, fn = (blocks,), hip.asmhip_matmul_q4_0 if fmt == "q4" else hip.asmhip_matmul_q8_0
+    dev = [DeviceBuffer.from_numpy(np.ascontiguousarray(p)) for p in planes]
+    dx, dy = DeviceBuffer.from_numpy(x), DeviceBuffer(M * 4)
+
+    def run(m):
+        # a prefix of rows is a prefix of every plane
+        assert fn(*[d.ptr for d in dev], dx.ptr, dy.ptr, m, K, None) == 0, hip.asmhip_last_error()
+        synchronize()
+        return dy.download(np.float32, m)
+
+    full = run(M)
+    if fmt[:2] == "q4":
+        w = oracle.dequantize_q4_0(blocks)
+        ref = oracle.matmul_q4_mt(*gguf.split_q4_0(blocks), x, NT)
+    else:
+        w = oracle.dequantize_q8_0(blocks)
+        ref = oracle.matmul_q8_0_gguf(blocks, x, NT)
+    assert_matvec_close(full, ref, w, x)
+    for m in TILE_HEIGHT_ROWS:
+        np.testing.assert_array_equal(run(m).view(np.uint32), full[:m].view(np.uint32), err_msg=f"m={m}")
+
+
 def test_bad_arguments_are_rejected(hip):
     dx, dy, db = DeviceBuffer(4096 * 4), DeviceBuffer(64 * 4), DeviceBuffer(64 * 128 * 18)
     assert hip.asmhip_matmul_q4_0(db.ptr, dx.ptr, dy.ptr, 64, 4010, None) == -1

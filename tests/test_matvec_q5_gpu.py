@@ -164,3 +164,18 @@ def test_q5_errors(hip):
     assert hip.asmhip_matmul_q5_0(p, p, p, 0, 64, None) == -1
     assert hip.asmhip_dequantize_q5_0(p, p, 1, 33, None) == -1
     assert "K % 32" in hip.asmhip_last_error().decode() or "K %% 32" in hip.asmhip_last_error().decode()
+
+
+@pytest.mark.parametrize("K", [2048, 4096])
+def test_q5_split_rows_do_not_depend_on_tile_height(hip, oracle, K):
+    """Split Q5 planes with at most one 8-row tile per compute unit run 8-row
+    tiles; the leading m rows of a 4096-row matrix (16-row tiles) give bitwise its
+    first m outputs, and the whole matrix stays within the bar of the oracle."""
+    M = 4096
+    ql, qh, d, x = _q5(K + 5, M, K)
+    s = d.astype(np.float32)
+    full = _split_device(hip, ql, qh, s, x)
+    assert_matvec_close(full, oracle.matmul_q5_mt(ql, qh, s, x, NT), ops_ref.dequantize_q5_0(ql, qh, s), x)
+    for m in (1, 7, 8, 9, 100, 1000, 2047, 2048, 2049):
+        y = _split_device(hip, ql[:m], qh[:m], s[:m], x)
+        np.testing.assert_array_equal(y.view(np.uint32), full[:m].view(np.uint32), err_msg=f"m={m}")
