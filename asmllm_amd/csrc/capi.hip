@@ -644,10 +644,9 @@ extern "C" int asmhip_matmul_attn_output(int qtype, const void* blocks, const fl
     if (!rc) rc = quant_type(qtype, &qt);
     if (rc) return rc;
     if (n_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return fail(kInvalidArgument, "bad attention shape");
+    if (max_ctx > kAttnMaxCtx)
+        return fail(kUnsupported, "attention output: max_ctx %d exceeds %d positions", max_ctx, kAttnMaxCtx);
     const int splits = attn_decode_splits(max_ctx);
-    if (splits > kAttnMaxSplits)
-        return fail(kUnsupported, "attention output: max_ctx %d exceeds %d positions", max_ctx,
-                    kAttnMaxSplits * kAttnSplitLen);
     const int64_t K = (int64_t)n_heads * head_dim;
     const hipStream_t st = (hipStream_t)stream;
     MatvecOpts o;
@@ -683,7 +682,7 @@ extern "C" int asmhip_matmul_attn_output(int qtype, const void* blocks, const fl
 // nothing needs clearing between calls; calls that overlap on one GPU share the
 // array and race.
 namespace {
-constexpr int64_t kNoAllocScratchFloats = 1 << 20;  // 4 MiB: n_heads * ceil(max_ctx / 512) * (head_dim + 4)
+constexpr int64_t kNoAllocScratchFloats = 1 << 20;  // 4 MiB: n_heads * splits * (head_dim + 4)
 __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 float* g_scratch_ptr[kMaxDevices] = {};
 

@@ -198,8 +198,8 @@ __global__ __launch_bounds__(kBlock) void attention_kernel(const float* __restri
 }
 
 // ---- decode attention over the fp16 cache: one launch per layer ----------------------
-// grid (n_heads, S = ceil(max_ctx / kAttnSplitLen)); workgroup (h, s) covers
-// positions [s*kAttnSplitLen, (s+1)*kAttnSplitLen) of 0..pos.  Within a workgroup
+// grid (n_heads, S = ceil(max_ctx / SL)), SL = attn_split_len(max_ctx); workgroup
+// (h, s) covers positions [s*SL, (s+1)*SL) of 0..pos.  Within a workgroup
 // a position is read by HD/8 lanes (8 dims = 16 bytes each), so a wave covers
 // 64/(HD/8) positions per row and the four waves kRowPos; a lane reads
 // kAttnRows rows of k and of v per chunk (one position each), and the split is
@@ -271,7 +271,7 @@ constexpr uint32_t kAttnPastEnd = 0xFFFFFF00u;  // buffer offset that loads zero
 
 enum RopeMode : int { kRopeNone = 0, kRopeTheta = 1, kRopeTable = 2 };
 
-template <int HD, int ROPE>
+template <int HD, int ROPE, int SL>
 __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __restrict__ qkv, __half* kc, __half* vc,
                                                              float* __restrict__ part, int n_heads, int n_kv,
                                                              const int* __restrict__ pos_ptr, int max_ctx,
@@ -283,8 +283,8 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     constexpr int kRowPos = kGroups * (kBlock / kWave);   // positions per workgroup and row
     constexpr int R = kAttnRows;                          // rows per lane and chunk
     constexpr int kChunkPos = kRowPos * R;
-    constexpr int kChunks = kAttnSplitLen / kChunkPos;
-    static_assert(kAttnSplitLen % kChunkPos == 0, "split must hold whole chunks");
+    constexpr int kChunks = SL / kChunkPos;
+    static_assert(SL % kChunkPos == 0, "split must hold whole chunks");
     constexpr int kStride = kAttnPartStride(HD);
     __shared__ float cs[HD];                 // cos, sin of pair i at 2i, 2i+1
     constexpr int kGroupsWg = kBlock / kLanes;  // lane groups (position slots) of the workgroup
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(const float* __rest
     const int group = n_heads / n_kv, kvh = h / group;
     const int pos = *pos_ptr;
     const int n_pos = (pos >= 0 && pos < max_ctx) ? pos + 1 : 0;  // an invalid position reads and writes nothing
-    const int p0 = split * kAttnSplitLen, p1 = min(p0 + kAttnSplitLen, n_pos);
+    const int p0 = split * SL, p1 = min(p0 + SL, n_pos);
     const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
     const int g = lane / kLanes, c = lane % kLanes;
     const size_t head_off = (size_t)kvh * max_ctx * HD + E * c;
@@ -626,26 +626,40 @@ int attention_launch(const float* q, const float* k, const float* v, float* y, i
     return kOk;
 }
 
-int attn_decode_splits(int max_ctx) { return (max_ctx + kAttnSplitLen - 1) / kAttnSplitLen; }
+int attn_decode_splits(int max_ctx) {
+    const int sl = attn_split_len(max_ctx);
+    return (int)(((int64_t)max_ctx + sl - 1) / sl);
+}
 
 int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx) {
     return (int64_t)n_heads * attn_decode_splits(max_ctx) * kAttnPartStride(hd);
 }
 
 namespace {
+template <int HD, int SL>
+void launch_attn_split(int mode, dim3 grid, hipStream_t st, const float* qkv, __half* kc, __half* vc, float* part,
+                       int n_heads, int n_kv, const int* pos_ptr, int max_ctx, float theta, const float* rope_table) {
+    if (mode == kRopeTable)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeTable, SL>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                           n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
+    else if (mode == kRopeTheta)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeTheta, SL>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                           n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
+    else
+        hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeNone, SL>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
+                           n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
+}
+
 template <int HD>
 void launch_attn_decode(int mode, dim3 grid, hipStream_t st, const float* qkv, __half* kc, __half* vc, float* part,
                         float* out, int n_heads, int n_kv, const int* pos_ptr, int max_ctx, float theta,
                         const float* rope_table) {
-    if (mode == kRopeTable)
-        hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeTable>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
-                           n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
-    else if (mode == kRopeTheta)
-        hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeTheta>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
-                           n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
+    if (attn_split_len(max_ctx) == kAttnSplitShort)
+        launch_attn_split<HD, kAttnSplitShort>(mode, grid, st, qkv, kc, vc, part, n_heads, n_kv, pos_ptr, max_ctx,
+                                               theta, rope_table);
     else
-        hipLaunchKernelGGL((attn_decode_kernel<HD, kRopeNone>), grid, dim3(kBlock), 0, st, qkv, kc, vc, part,
-                           n_heads, n_kv, pos_ptr, max_ctx, theta, rope_table);
+        launch_attn_split<HD, kAttnSplitLong>(mode, grid, st, qkv, kc, vc, part, n_heads, n_kv, pos_ptr, max_ctx,
+                                              theta, rope_table);
     if (out) hipLaunchKernelGGL((attn_decode_merge<HD>), dim3(n_heads), dim3(HD), 0, st, part, out, (int)grid.y);
 }
 }  // namespace
@@ -655,10 +669,9 @@ int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* pa
                        const float* rope_table) {
     if (n_kv <= 0 || n_heads % n_kv) return fail(kInvalidArgument, "attention: n_heads %% n_kv_heads != 0");
     if (max_ctx <= 0) return fail(kInvalidArgument, "attention: max_ctx must be > 0");
+    if (max_ctx > kAttnMaxCtx)
+        return fail(kUnsupported, "attention: max_ctx %d exceeds %d positions", max_ctx, kAttnMaxCtx);
     const int splits = attn_decode_splits(max_ctx);
-    if (splits > kAttnMaxSplits)
-        return fail(kUnsupported, "attention: max_ctx %d exceeds %d positions", max_ctx,
-                    kAttnMaxSplits * kAttnSplitLen);
     if ((uintptr_t)qkv % 16 || (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16 || (uintptr_t)part % 16)
         return fail(kInvalidArgument, "attention: q, the caches and the workspace must be 16-byte aligned");
     if (rope_table && (uintptr_t)rope_table % 8)
@@ -686,10 +699,9 @@ int attn_decode_launch(const float* qkv, void* k_cache, void* v_cache, float* pa
 
 int attn_merge_launch(const float* part, float* out, int n_heads, int hd, int max_ctx, hipStream_t st) {
     if (n_heads <= 0 || max_ctx <= 0) return fail(kInvalidArgument, "attention merge: bad shape");
+    if (max_ctx > kAttnMaxCtx)
+        return fail(kUnsupported, "attention merge: max_ctx %d exceeds %d positions", max_ctx, kAttnMaxCtx);
     const int splits = attn_decode_splits(max_ctx);
-    if (splits > kAttnMaxSplits)
-        return fail(kUnsupported, "attention merge: max_ctx %d exceeds %d positions", max_ctx,
-                    kAttnMaxSplits * kAttnSplitLen);
     if (hd == 128)
         hipLaunchKernelGGL((attn_decode_merge<128>), dim3(n_heads), dim3(128), 0, st, part, out, splits);
     else if (hd == 64)

@@ -120,16 +120,26 @@ int attention_launch(const float* q, const float* k, const float* v, float* y, i
                      hipStream_t st);
 
 // Decode attention over head-major fp16 caches [n_kv][max_ctx][hd], positions
-// 0..*pos_ptr: kAttnSplitLen-position splits, each walked in chunks of
+// 0..*pos_ptr: attn_split_len(max_ctx)-position splits, each walked in chunks of
 // kAttnRows rows per lane, then a merge launch (out != nullptr) or nothing (the
 // partials are left for a matvec with kPreAttnMerge).  `part` holds
 // attn_decode_workspace() floats: per head and split [m, l, -, -, acc[hd]]
 // (kAttnPartStride(hd) floats).  rope = true rotates q and the new k at
 // *pos_ptr and writes the new k/v rows (fp16) in the split launch.
-constexpr int kAttnSplitLen = 512;
 constexpr int kAttnRows = 4;
 constexpr int kAttnMaxSplits = 64;
-constexpr int kAttnMergeMaxSplits = 8;  // splits a matvec merges in its x prologue (max_ctx <= 4096)
+constexpr int kAttnMergeMaxSplits = 8;  // splits a matvec merges in its x prologue
+// Split length: 384 positions while that keeps the splits within what a matvec
+// merges (max_ctx <= 3072), else 512 (max_ctx <= 32768).  Shorter splits put
+// more workgroups on the cache stream (7B, context 2048, max_ctx 2176: 6 splits
+// of 384 give split attention + o projection 14.99 us per layer, 5 of 512 15.52;
+// 320 positions, 7 splits, 15.18; 256, 9 splits, 18.2).  Both are whole chunks
+// for every head_dim (64 or 128 positions per chunk).
+constexpr int kAttnSplitShort = 384, kAttnSplitLong = 512;
+constexpr int kAttnMaxCtx = kAttnMaxSplits * kAttnSplitLong;
+constexpr int attn_split_len(int max_ctx) {
+    return max_ctx <= kAttnMergeMaxSplits * kAttnSplitShort ? kAttnSplitShort : kAttnSplitLong;
+}
 constexpr int kAttnPartStride(int hd) { return hd + 4; }
 int attn_decode_splits(int max_ctx);
 int64_t attn_decode_workspace(int n_heads, int hd, int max_ctx);

@@ -22,8 +22,8 @@ stream, so it can be captured once into a HIP graph and replayed per token:
   * RoPE and the KV-cache write are fused into the attention launch
     (asmhip_attention_decode_partials_rope_table), its cos/sin read from a
     table of every position's angles formed once at set-up
-    (asmhip_rope_table); the attention leaves its 512-position splits'
-    softmax states in a workspace, and the o matvec merges them as it reads
+    (asmhip_rope_table); the attention leaves its splits' (384 or 512
+    positions) softmax states in a workspace, and the o matvec merges them as it reads
     its x (asmhip_matmul_attn_output), so attention + o take two launches;
   * the KV cache is fp16, head-major [n_kv_heads][max_ctx][head_dim] per layer
     (the reference keeps fp32 [128][heads][head_dim], generate.py:252-253);

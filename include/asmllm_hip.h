@@ -243,7 +243,8 @@ ASMHIP_API int asmhip_attention_decode_rope_table(const float* qkv, void* k_cach
  * three (generate.py:283-300: per-head softmax(q k^T) v, then the o matvec and
  * the residual add).  asmhip_attention_decode_partials_rope_table is
  * asmhip_attention_decode_rope_table without its merge launch: it leaves every
- * 512-position split's softmax state in `workspace`
+ * split's softmax state in `workspace` (splits of 384 positions while
+ * max_ctx <= 3072, else of 512)
  * (asmhip_attention_decode_workspace() floats, 16-byte aligned).
  * asmhip_matmul_attn_output then computes y = W . attn (accumulate: y += W .
  * attn) for GGUF blocks W [M][n_heads * head_dim / 32] (qtype Q4_0 or Q8_0),
@@ -271,7 +272,8 @@ ASMHIP_API int asmhip_stream_read(const void* buf, int64_t bytes, void* sink, vo
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
  * split partials go to a fixed per-device scratch array of
  * asmhip_attention_decode_noalloc_max_floats() floats (4 MiB); shapes needing
- * more (n_heads * ceil(max_ctx / 512) * (head_dim + 4) floats) are rejected with
+ * more (n_heads * S * (head_dim + 4) floats, S = ceil(max_ctx / 384) for
+ * max_ctx <= 3072, else ceil(max_ctx / 512)) are rejected with
  * ASMHIP_ERR_INVALID_ARGUMENT.  Calls that overlap on one GPU share the array and
  * race; nothing in it needs clearing between calls.  Same results, bit for bit,
  * as asmhip_attention_decode_rope. */

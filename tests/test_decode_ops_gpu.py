@@ -136,9 +136,12 @@ def _random_attention_cases(n, seed):
     (32, 8, 128, 128, 300), (4, 4, 128, 127, 128), (8, 8, 64, 8191, 8192),
     # head_dim 48 (stories15M): one split, several, and 64 splits (more than the merge's 48 threads)
     (6, 6, 48, 5, 64), (6, 6, 48, 300, 2048), (6, 2, 48, 8000, 8192),
-    # split (512 positions) and chunk (64 / 128 positions) boundaries, a split
-    # holding only pos, and a cache of 64 splits (the most the merge takes)
-    (4, 4, 128, 511, 600), (4, 2, 128, 512, 600), (4, 4, 128, 513, 1100), (4, 4, 128, 63, 64),
+    # split (384 positions up to max_ctx 3072, 512 above) and chunk (64 / 128
+    # positions) boundaries, a split holding only pos, the most splits a matvec
+    # merges (8), and a cache of 64 splits (the most the merge launch takes)
+    (4, 4, 128, 383, 600), (4, 2, 128, 384, 600), (4, 4, 128, 385, 800), (6, 6, 48, 767, 800),
+    (8, 4, 64, 768, 1000), (4, 4, 128, 3071, 3072), (4, 4, 128, 511, 3073), (4, 2, 128, 512, 3200),
+    (4, 4, 128, 513, 4096), (4, 4, 128, 511, 600), (4, 4, 128, 513, 1100), (4, 4, 128, 63, 64),
     (4, 4, 128, 64, 130), (8, 4, 64, 127, 1024), (6, 6, 48, 1535, 1537), (2, 1, 128, 32767, 32768),
 ] + _random_attention_cases(8, 77))
 def test_rope_kv_write_and_decode_attention(hip, oracle, n_heads, n_kv, hd, pos, max_ctx):
@@ -369,6 +372,8 @@ def test_argmax_non_finite_as_numpy(hip, n, case):
     (32, 32, 128, 2048, 2176, 4096),   # the 7B step: the merge inside the int8-MFMA matvec
     (8, 2, 64, 300, 1024, 384),        # K = 512: the MFMA stream with its x from LDS
     (16, 4, 128, 5000, 6000, 200),     # 12 splits: more than are requested up front
+    (16, 16, 128, 3071, 3072, 1024),   # 8 splits of 384 positions: the most the matvec merges
+    (16, 16, 128, 3072, 3073, 1024),   # past 3072: 7 splits of 512
     (16, 16, 64, 0, 100, 32),          # one position, one split
     (6, 6, 48, 100, 256, 288),         # K = 288 (stories15M): merge launch + matvec
 ])
