@@ -35,7 +35,8 @@
 //
 // Work mapping (persistent stream): one workgroup of NW waves per compute
 // unit.  Workgroup b owns the 16-row tiles b, b + G, b + 2G, ... (G = grid
-// size); a tile's K is cut into 8-block units (16 rows x 144 bytes), and wave w
+// size; small Q8_0 / split-layout matvecs use 8-row tiles, the upper 8 MFMA
+// rows zero); a tile's K is cut into 8-block units (16 rows x 144 bytes), and wave w
 // takes units w, w + NW, ... of every tile in turn, so each wave walks one long
 // sequence of units.  D units of loads stay in flight per wave (coalesced
 // 16-byte buffer loads; past the end of the sequence the offset is pushed
@@ -381,8 +382,8 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     const uint32_t row_bytes4 = (uint32_t)nb * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int G = gridDim.x;
-    // tiles of TH rows (16, or 8 for small Q8_0 matvecs); MFMA rows TH..15 of
-    // a tile load zeros
+    // tiles of TH rows (16, or 8 for small Q8_0 and split-layout matvecs); MFMA
+    // rows TH..15 of a tile load zeros and are not written
     static_assert(TH == 16 || TH == 8, "tile height");
     const int n_tiles = (M + TH - 1) >> (TH == 16 ? 4 : 3);
     const int my_tiles = (n_tiles - (int)blockIdx.x + G - 1) / G;
@@ -735,7 +736,7 @@ size_t stream_lds(int slot_bytes, int nw, int nb, int tiles_per_group) {
     return (size_t)nw * slot_bytes + (size_t)nb * (kXStride + 4) + (size_t)tiles_per_group * nw * 16 * sizeof(float);
 }
 
-// Workgroup layout for tiles of th rows (16; 8 for the small Q8_0 matvecs, see mfma_launch).
+// Workgroup layout for tiles of th rows (16; 8 for small Q8_0 and split-layout matvecs, see mfma_launch).
 StreamShape stream_shape(int slot_bytes, int64_t M, int64_t K, int th = 16) {
     const int nb = (int)(K / 32);
     const int cus = compute_units();
