@@ -110,6 +110,30 @@ def test_graph_replay_matches_eager_launches():
     eng.close()
 
 
+@pytest.mark.parametrize("max_ctx,pos0", [(800, 381), (3100, 1021)], ids=["384-splits", "512-splits"])
+def test_steps_across_attention_split_boundaries(max_ctx, pos0):
+    """Steps whose positions cross a split boundary of the decode attention
+    (max_ctx 800: 384-position splits, 3 of them; max_ctx 3100: 512-position
+    splits, 7): every step within the bar of the oracle, and a graph replay of
+    the same steps equal to the eager launches bit for bit."""
+    eng = DecodeEngine(SMALL[1], max_ctx=max_ctx)
+    eng.init_random(seed=11)
+    ref = _oracle_model(eng, nt=4)
+    token = 3
+    for step in range(5):
+        pos = pos0 + step
+        got = eng.forward_token(token, pos)
+        want = ref.forward_token(token, pos)
+        _check_logits(got, want, f"max_ctx {max_ctx} pos {pos}")
+        token = int(np.argmax(want))
+    eager = eng.generate(3, pos0, 5, use_graph=False)
+    logits_eager = eng.logits.download(np.float32, SMALL[1].vocab)
+    graphed = eng.generate(3, pos0, 5, use_graph=True)
+    assert graphed == eager
+    np.testing.assert_array_equal(eng.logits.download(np.float32, SMALL[1].vocab), logits_eager)
+    eng.close()
+
+
 def test_engine_rejects_positions_outside_the_cache():
     eng = DecodeEngine(SMALL[0], max_ctx=16)
     with pytest.raises(ValueError):
