@@ -841,6 +841,16 @@ extern "C" void* asmhip_event_create(void) {
     return (void*)e;
 }
 
+extern "C" void* asmhip_event_create_timing(void) {
+    hipEvent_t e = nullptr;
+    hipError_t r = hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
+    if (r != hipSuccess) {
+        hip_fail(r, "hipEventCreateWithFlags");
+        return nullptr;
+    }
+    return (void*)e;
+}
+
 extern "C" int asmhip_event_destroy(void* event) {
     if (!event) return kOk;
     ASMHIP_TRY(hipEventDestroy((hipEvent_t)event));

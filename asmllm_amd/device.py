@@ -86,8 +86,12 @@ class Stream:
 
 
 class Event:
-    def __init__(self):
-        handle = lib().asmhip_event_create()
+    """A HIP event.  timing=True: an event used only to time stream work
+    (asmhip_event_create_timing): its record does no system-scope cache
+    writeback / invalidate, which would otherwise slow the work after it."""
+
+    def __init__(self, timing: bool = False):
+        handle = lib().asmhip_event_create_timing() if timing else lib().asmhip_event_create()
         if not handle:
             check(-2, "event create")
         self.handle = int(handle)

@@ -94,6 +94,7 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_stream_destroy": (c_int, [_P]),
     "asmhip_stream_synchronize": (c_int, [_P]),
     "asmhip_event_create": (c_void_p, []),
+    "asmhip_event_create_timing": (c_void_p, []),
     "asmhip_event_destroy": (c_int, [_P]),
     "asmhip_event_record": (c_int, [_P, _P]),
     "asmhip_event_synchronize": (c_int, [_P]),

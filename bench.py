@@ -117,6 +117,7 @@ def bench_matvec(steps: int, warmup: int, copies: int) -> dict:
         b.copy_from(bufs[0])
         bufs.append(b)
     dx, dy = DeviceBuffer.from_numpy(x), DeviceBuffer(M * 4)
+    cov, sink = DeviceBuffer(1 << 30), DeviceBuffer(4096)  # untimed cover reads (see timed)
     stream = Stream()
 
     def launch(i: int) -> None:
@@ -138,38 +139,71 @@ def bench_matvec(steps: int, warmup: int, copies: int) -> dict:
     log(f"parity ok (max err / row L1 {worst:.2e})")
 
     def timed(n_steps: int) -> tuple[float, float]:
-        """GPU ms and wall s of exactly `n_steps` launches: graphs over all
-        copies plus one graph for the remainder, between HIP events on the
-        launch stream, with device synchronizations before the warm-up and
-        after the timed steps.  The last warm-up round is enqueued right before
-        the start event, so the GPU is still busy with it while the host
-        submits the timed graphs: the timed region holds the K launches and no
-        host submission latency (which is ~5 us per graph launch from an idle
-        GPU, 0.25 us a step at K = 20)."""
-        graph = Graph.capture(stream, lambda: [launch(i) for i in range(copies)])
-        rem = n_steps % copies
-        graph_rem = Graph.capture(stream, lambda: [launch(i) for i in range(rem)]) if rem else None
+        """GPU ms and wall s of exactly `n_steps` launches between two HIP
+        events on the launch stream, with device synchronizations before the
+        last untimed round and after the timed steps.
+
+        A HIP graph launch costs ~7 us before its first kernel starts, also when
+        it is queued behind running work (measured: 640 steps as 20 graphs of 32
+        launches 7.06 us a step, as one graph 6.79), so the timed region keeps
+        graph boundaries out or few: up to 512 steps are plain stream launches,
+        enqueued while the GPU still runs untimed single-launch reads
+        (asmhip_stream_read, one host call each) long enough (~40 us of host
+        time per launch) that all K launches are queued before the start event
+        fires (after one untimed pass of the same launches: the first such pass
+        runs slower); more steps are graphs of 512 launches (one
+        boundary per 512 steps, ~0.01 us a step; one graph serves every full
+        block of 512, cycling over the copies), each graph launched once
+        untimed first (a graph's first launch also sets it up).  The
+        events are timing-only (hipEventDisableSystemFence, HIP's flag for
+        events that only measure time: no system-scope cache writeback and
+        invalidate at record)."""
+        e0, e1 = Event(timing=True), Event(timing=True)
+        warm = Graph.capture(stream, lambda: [launch(i) for i in range(copies)])
+
+        def cover() -> None:
+            # untimed single-launch reads (~160 us per GiB) that keep the GPU busy
+            # while the host enqueues the timed launches (~40 us of host time each)
+            for _ in range(1 + -(-n_steps * 40 // 150)):
+                native.check(lib.asmhip_stream_read(cov.ptr, cov.nbytes, sink.ptr, stream.handle), "cover read")
+
+        big = []  # graphs of the timed region, in order
+        if n_steps > 512:
+            full = Graph.capture(stream, lambda: [launch(i % copies) for i in range(512)])
+            big = [full] * (n_steps // 512)
+            rem = n_steps % 512
+            if rem:
+                big.append(Graph.capture(stream, lambda: [launch((n_steps - rem + i) % copies) for i in range(rem)]))
         for _ in range(max(1, -(-warmup // copies))):
-            graph.launch(stream)
-        if graph_rem:  # a graph's first launch also sets it up on the device
-            graph_rem.launch(stream)
+            warm.launch(stream)
+        for g in dict.fromkeys(big):  # each graph once
+            g.launch(stream)
         synchronize()
-        e0, e1 = Event(), Event()
+        if not big:  # one untimed pass of the same stream launches (first passes run slower)
+            cover()
+            for i in range(n_steps):
+                launch(i % copies)
+            synchronize()
         t0 = time.perf_counter()
-        graph.launch(stream)  # untimed: keeps the GPU busy while the timed graphs are submitted
+        if big:
+            warm.launch(stream)
+        else:
+            cover()
         e0.record(stream)
-        for _ in range(n_steps // copies):
-            graph.launch(stream)
-        if graph_rem:
-            graph_rem.launch(stream)
+        if big:
+            for g in big:
+                g.launch(stream)
+        else:
+            for i in range(n_steps):
+                launch(i % copies)
         e1.record(stream)
         e1.synchronize()
         synchronize()
         wall = time.perf_counter() - t0
         ms = e0.elapsed_ms(e1)
-        graph.close()
-        if graph_rem:
-            graph_rem.close()
+        warm.close()
+        for g in dict.fromkeys(big):
+            g.close()
         return ms, wall
 
     total_ms, wall_s = timed(steps)
@@ -324,7 +358,7 @@ def time_launches(enqueue, copies: int, reps: int) -> float:
     for _ in range(2):
         run()
     synchronize()
-    e0, e1 = Event(), Event()
+    e0, e1 = Event(timing=True), Event(timing=True)
     e0.record(stream)
     for _ in range(reps):
         run()
@@ -647,7 +681,7 @@ def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: 
     eng.stream.synchronize()
     eng.set_position(1, context)
     synchronize()
-    e0, e1 = Event(), Event()
+    e0, e1 = Event(timing=True), Event(timing=True)
     e0.record(eng.stream)
     for _ in range(steps):
         step()

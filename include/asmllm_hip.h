@@ -308,6 +308,10 @@ ASMHIP_API void* asmhip_stream_create(void);
 ASMHIP_API int asmhip_stream_destroy(void* stream);
 ASMHIP_API int asmhip_stream_synchronize(void* stream);
 ASMHIP_API void* asmhip_event_create(void);
+/* An event for timing only (hipEventDisableSystemFence): recording it does no
+ * system-scope cache writeback / invalidate, so it does not perturb the work
+ * that follows; waiting on it does not make device writes visible to the host. */
+ASMHIP_API void* asmhip_event_create_timing(void);
 ASMHIP_API int asmhip_event_destroy(void* event);
 ASMHIP_API int asmhip_event_record(void* event, void* stream);
 ASMHIP_API int asmhip_event_synchronize(void* event);
