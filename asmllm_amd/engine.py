@@ -376,6 +376,16 @@ class DecodeEngine:
             self._graph = Graph.capture(self.stream, self.enqueue_step)
         return self._graph
 
+    def capture_steps(self, n_steps: int) -> Graph:
+        """n_steps consecutive token steps as one HIP graph (the caller closes it).
+        Each step reads the token and position the previous one left on the GPU,
+        so one replay decodes n_steps tokens with one graph launch instead of
+        n_steps (a graph launch costs ~7 us before its first kernel starts); the
+        intermediate tokens are not kept, the last one is in `token`."""
+        if n_steps < 1:
+            raise ValueError("n_steps must be >= 1")
+        return Graph.capture(self.stream, lambda: [self.enqueue_step() for _ in range(n_steps)])
+
     def generate(self, token_id: int, pos: int, n_steps: int, use_graph: bool = True) -> list[int]:
         """Greedy decode of n_steps tokens starting from token_id at pos
         (the loop of generate.py:411-430, argmax on the GPU)."""

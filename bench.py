@@ -341,30 +341,38 @@ EAGER = False  # --eager: launch directly instead of replaying graphs
 
 
 def time_launches(enqueue, copies: int, reps: int) -> float:
-    """Mean GPU microseconds of one launch: `enqueue(i)` for i < copies captured
-    into one graph, replayed `reps` times between HIP events."""
+    """Mean GPU microseconds of one launch: `enqueue(i)` cycling over i < copies,
+    at least reps x copies launches, between timing-only HIP events.  The
+    launches are captured into graphs of at least 512 (a whole number of
+    rounds over the copies), since every graph launch costs ~7 us before its
+    first kernel starts: in graphs of `copies` launches that would add
+    7 us / copies to each launch."""
     from asmllm_amd.device import Event, Graph, Stream, synchronize
 
     stream = Stream()
+    rounds = max(1, -(-512 // copies))  # rounds over the copies per graph
     if EAGER:
         def run():
-            for i in range(copies):
-                enqueue(i, stream.handle)
+            for _ in range(rounds):
+                for i in range(copies):
+                    enqueue(i, stream.handle)
     else:
-        graph = Graph.capture(stream, lambda: [enqueue(i, stream.handle) for i in range(copies)])
+        graph = Graph.capture(stream, lambda: [enqueue(i, stream.handle) for _ in range(rounds)
+                                               for i in range(copies)])
 
         def run():
             graph.launch(stream)
     for _ in range(2):
         run()
     synchronize()
+    runs = max(1, -(-reps // rounds))
     e0, e1 = Event(timing=True), Event(timing=True)
     e0.record(stream)
-    for _ in range(reps):
+    for _ in range(runs):
         run()
     e1.record(stream)
     e1.synchronize()
-    us = e0.elapsed_ms(e1) * 1e3 / (reps * copies)
+    us = e0.elapsed_ms(e1) * 1e3 / (runs * rounds * copies)
     if not EAGER:
         graph.close()
     return us
@@ -517,7 +525,7 @@ def bench_read_floor(multiples=(1, 2, 4, 8)) -> dict:
     slope, fixed = np.polyfit(xs, ys, 1)
 
     # the same kernel on 4 KB (one 16-byte load per workgroup): what a dependent
-    # graph node costs with next to no work, in graphs of 64 launches
+    # graph node costs with next to no work (64 addresses cycled in graphs of 512 launches)
     def enqueue_tiny(i, st):
         native.check(lib.asmhip_stream_read(buf.ptr + i * 4096, 4096, sink.ptr, st), "stream read")
 
@@ -657,9 +665,11 @@ def decode_cpu_baseline(eng, context: int, seconds: float) -> dict:
 def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: bool = False,
                  cpu_seconds: float = 0.0) -> dict:
     """Greedy single-token decode of the 32-layer 7B-shape Q4_0 model, fp16 KV
-    cache prefilled to `context`: `steps` tokens from position `context`,
-    each one replay of the captured token-step graph (token and position stay
-    on the GPU between steps).  `eager` enqueues the launches directly instead
+    cache prefilled to `context`: `steps` tokens from position `context`, as
+    replays of a captured graph of 16 consecutive token steps (token and
+    position stay on the GPU between steps; one graph launch per 16 tokens,
+    since a graph launch costs ~7 us before its first kernel) plus single-step
+    replays for the remainder.  `eager` enqueues the launches directly instead
     (for tracing tools that do not follow graph launches)."""
     from asmllm_amd.device import Event, synchronize
     from asmllm_amd.engine import LLAMA_7B, DecodeEngine
@@ -667,10 +677,13 @@ def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: 
     s = LLAMA_7B
     eng = DecodeEngine(s, max_ctx=context + steps)
     eng.init_random(seed=42)
+    per_graph = 16
+    multi = None
     if eager:
         step = eng.enqueue_step
     else:
         graph = eng.capture()
+        multi = eng.capture_steps(per_graph) if steps >= per_graph else None
 
         def step():
             graph.launch(eng.stream)
@@ -678,16 +691,25 @@ def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: 
     eng.set_position(1, context)
     for _ in range(warmup):
         step()
+    if multi is not None:  # a graph's first launch also sets it up on the device
+        multi.launch(eng.stream)
     eng.stream.synchronize()
     eng.set_position(1, context)
     synchronize()
     e0, e1 = Event(timing=True), Event(timing=True)
     e0.record(eng.stream)
-    for _ in range(steps):
+    done = 0
+    if multi is not None:
+        for _ in range(steps // per_graph):
+            multi.launch(eng.stream)
+        done = steps // per_graph * per_graph
+    for _ in range(steps - done):
         step()
     e1.record(eng.stream)
     e1.synchronize()
     ms = e0.elapsed_ms(e1)
+    if multi is not None:
+        multi.close()
     end_pos = eng.read_position()
     if end_pos != context + steps:
         raise SystemExit(f"decode: position {end_pos} after {steps} steps from {context}")

@@ -134,6 +134,26 @@ def test_steps_across_attention_split_boundaries(max_ctx, pos0):
     eng.close()
 
 
+def test_multi_step_graph_matches_single_step_replays():
+    """A graph of 5 consecutive token steps (capture_steps) leaves the same
+    token, position and logits, bit for bit, as 5 replays of the one-step graph."""
+    shape = SMALL[2]
+    eng = DecodeEngine(shape, max_ctx=64)
+    eng.init_random(seed=5)
+    single = eng.generate(7, 20, 5, use_graph=True)
+    logits_single = eng.logits.download(np.float32, shape.vocab)
+    assert eng.read_position() == 25
+    multi = eng.capture_steps(5)
+    eng.set_position(7, 20)
+    multi.launch(eng.stream)
+    eng.stream.synchronize()
+    assert eng.read_position() == 25
+    assert int(eng.token.download(np.int32, (1,))[0]) == single[-1]
+    np.testing.assert_array_equal(eng.logits.download(np.float32, shape.vocab), logits_single)
+    multi.close()
+    eng.close()
+
+
 def test_engine_rejects_positions_outside_the_cache():
     eng = DecodeEngine(SMALL[0], max_ctx=16)
     with pytest.raises(ValueError):
