@@ -162,10 +162,12 @@ def bench_matvec(steps: int, warmup: int, copies: int) -> dict:
         warm = Graph.capture(stream, lambda: [launch(i) for i in range(copies)])
 
         def cover() -> None:
-            # untimed single-launch reads (~160 us per GiB; at least 20, ~3 ms) that
-            # keep the GPU busy while the host enqueues the timed launches (~40 us
-            # of host time each, with margin for host-side stalls)
-            for _ in range(max(20, 1 + -(-n_steps * 40 // 150))):
+            # untimed single-launch reads (~160 us per GiB) that keep the GPU busy
+            # while the host enqueues the timed launches (~40 us of host time
+            # each), at least 400 (~64 ms): the GPU reaches its steady speed only
+            # after tens of ms of load (20 steps behind 3 / 16 / 64 ms of reads:
+            # 6.95 / 6.80 / 6.74 us a step, the last as in 4096-step runs)
+            for _ in range(max(400, 1 + -(-n_steps * 40 // 150))):
                 native.check(lib.asmhip_stream_read(cov.ptr, cov.nbytes, sink.ptr, stream.handle), "cover read")
 
         big = []  # graphs of the timed region, in order
