@@ -129,6 +129,15 @@ struct AttnMergeQuads {
             ac[i][1] = *reinterpret_cast<const float4*>(e + 20 + t);
         }
     }
+    // the acc values only (the caller fills ml)
+    __device__ __forceinline__ void load_acc(const float* ph, int stride, int t) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const float* e = ph + (size_t)i * stride;
+            ac[i][0] = *reinterpret_cast<const float4*>(e + 4 + t);
+            ac[i][1] = *reinterpret_cast<const float4*>(e + 20 + t);
+        }
+    }
 
     __device__ __forceinline__ void finish(float4* lo, float4* hi) const {
         float M = -INFINITY;

@@ -448,6 +448,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     float4 xv[XQ][2], av[XQ][2];
     constexpr bool AM = AMS > 0;
     AttnMergeQuads<AM ? AMS : 1> am;
+    float2 sml[AM ? 4 : 1][AM ? AMS : 1];  // head_dim 128: the (m, l) of the wave's 4 heads, per split
     // waves holding x items (a wave-uniform test: in a wave past the last item
     // no load is issued, in the others every lane loads)
     const bool am_items = wave * 64 < ni;
@@ -456,7 +457,24 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         const int it = min((int)threadIdx.x, ni - 1);
         const int off = 32 * (it >> 2) + 4 * (it & 3);  // positions off.. and off + 16.. of one head
         const int hh = off / pre_hd;
-        if (am_items) am.load(pre_arg + (size_t)hh * AMS * (pre_hd + 4), pre_hd + 4, off - hh * pre_hd);
+        const float* ph = pre_arg + (size_t)hh * AMS * (pre_hd + 4);
+        if (am_items && pre_hd == 128) {
+            // head_dim 128: a wave's 64 items are 4 heads of 16 lanes.  The acc
+            // values are requested per lane; each split's (m, l) of the four heads
+            // comes through wave-uniform scalar loads, picked per 16-lane group
+            // only after the weights are requested (64-lane loads of (m, l), 16
+            // lanes on each address, cost ~0.8 us a launch at 6 splits).
+            am.load_acc(ph, 128 + 4, off - hh * 128);
+            const int nh = ni >> 4, h0 = wave * 4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < AMS; ++i)
+                    sml[j][i] = *reinterpret_cast<const float2*>(
+                        pre_arg + ((size_t)min(h0 + j, nh - 1) * AMS + i) * (128 + 4));
+        } else if (am_items) {
+            am.load(ph, pre_hd + 4, off - hh * pre_hd);
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < XQ; ++i) {
@@ -481,6 +499,20 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     // 3) fused pre-op on x, then digits; partial sums start at zero.
     for (int i = threadIdx.x; i < my_tiles * NW * 16; i += kThreads) part[i] = 0.f;
     if constexpr (AM) {
+        if (am_items && pre_hd == 128) {
+            // branch-free pick of head lane >> 4 of the four: bitwise selects on the
+            // bit patterns (exact for every value, -inf included)
+            const uint32_t b16 = 0u - (uint32_t)((lane >> 4) & 1), b32 = 0u - (uint32_t)((lane >> 5) & 1);
+            auto pick = [&](float f0, float f1, float f2, float f3) {
+                const uint32_t lo = (b16 & __float_as_uint(f1)) | (~b16 & __float_as_uint(f0));
+                const uint32_t hi = (b16 & __float_as_uint(f3)) | (~b16 & __float_as_uint(f2));
+                return __uint_as_float((b32 & hi) | (~b32 & lo));
+            };
+#pragma unroll
+            for (int i = 0; i < AMS; ++i)
+                am.ml[i] = make_float2(pick(sml[0][i].x, sml[1][i].x, sml[2][i].x, sml[3][i].x),
+                                       pick(sml[0][i].y, sml[1][i].y, sml[2][i].y, sml[3][i].y));
+        }
         if (am_items) am.finish(&xv[0][0], &xv[0][1]);
         else xv[0][0] = xv[0][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // no item: no digit writes below
     } else if (pre == kPreRmsNorm) {
