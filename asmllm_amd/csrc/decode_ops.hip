@@ -507,6 +507,10 @@ __device__ __forceinline__ bool argmax_better(float a, int ia, float b, int ib) 
     return a > b || (a == b && ia < ib);
 }
 
+// VEC (n % 4 == 0, logits 16-byte aligned): 16-byte loads, 8 per thread and
+// pass instead of 32 single floats; which thread sees an element does not
+// change the result (ties go to the lower index).
+template <bool VEC>
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
                                                       int* __restrict__ token, int* __restrict__ pos) {
     __shared__ float bv[16];
@@ -518,17 +522,36 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
     constexpr int kPer = 32;
     for (int base = 0; base < n; base += kPer * 1024) {
         float x[kPer];
+        if constexpr (VEC) {
+            // element base + 4 (k 1024 + t) + j of load k, lane j
 #pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            const int i = base + k * 1024 + (int)threadIdx.x;
-            x[k] = i < n ? logits[i] : -INFINITY;
-        }
+            for (int k = 0; k < kPer / 4; ++k) {
+                const int i = base + 4 * (k * 1024 + (int)threadIdx.x);
+                const float4 q = i < n ? *reinterpret_cast<const float4*>(logits + i)
+                                       : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+                x[4 * k] = q.x, x[4 * k + 1] = q.y, x[4 * k + 2] = q.z, x[4 * k + 3] = q.w;
+            }
 #pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            const int i = base + k * 1024 + (int)threadIdx.x;
-            if (i < n && argmax_better(x[k], i, v, idx)) {
-                v = x[k];
-                idx = i;
+            for (int k = 0; k < kPer; ++k) {
+                const int i = base + 4 * ((k >> 2) * 1024 + (int)threadIdx.x) + (k & 3);
+                if (i < n && argmax_better(x[k], i, v, idx)) {
+                    v = x[k];
+                    idx = i;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int i = base + k * 1024 + (int)threadIdx.x;
+                x[k] = i < n ? logits[i] : -INFINITY;
+            }
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int i = base + k * 1024 + (int)threadIdx.x;
+                if (i < n && argmax_better(x[k], i, v, idx)) {
+                    v = x[k];
+                    idx = i;
+                }
             }
         }
     }
@@ -747,7 +770,10 @@ int embed_launch(QuantType qt, const void* table, const int* token, float* x, in
 
 int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st) {
     if (n <= 0) return fail(kInvalidArgument, "argmax: empty input");
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, st, logits, n, token, pos);
+    if (n % 4 == 0 && (uintptr_t)logits % 16 == 0)
+        hipLaunchKernelGGL(argmax_kernel<true>, dim3(1), dim3(1024), 0, st, logits, n, token, pos);
+    else
+        hipLaunchKernelGGL(argmax_kernel<false>, dim3(1), dim3(1024), 0, st, logits, n, token, pos);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

@@ -249,10 +249,11 @@ def test_embed_row_and_argmax(hip, oracle):
     assert int(dpos.download(np.int32, 1)[0]) == 42
 
 
-@pytest.mark.parametrize("n", [1, 5, 1024, 32000, 32768, 32769, 128256])
+@pytest.mark.parametrize("n", [1, 5, 36, 1024, 32000, 32768, 32769, 128256])
 def test_argmax_sizes_and_ties(hip, n):
-    """One pass (n <= 32768) and several (the Llama-3 vocabulary); a tie across
-    passes and lanes resolves to the first index, as numpy.argmax."""
+    """One pass (n <= 32768) and several (the Llama-3 vocabulary), with 16-byte
+    loads (n % 4 == 0) and single floats; a tie across passes and lanes resolves
+    to the first index, as numpy.argmax."""
     rng = np.random.default_rng(n)
     logits = rng.standard_normal(n).astype(np.float32)
     if n > 2:
@@ -339,7 +340,7 @@ def test_decode_attention_outside_the_cache_is_zero(hip, pos, rope):
     np.testing.assert_array_equal(dqkv.download(np.float32, qkv.size), qkv)
 
 
-@pytest.mark.parametrize("n", [5, 1024, 32769])
+@pytest.mark.parametrize("n", [5, 1024, 32000, 32769])
 @pytest.mark.parametrize("case", ["all-nan", "one-nan", "two-nan", "all-neg-inf", "neg-inf-and-one", "two-pos-inf"])
 def test_argmax_non_finite_as_numpy(hip, n, case):
     """numpy.argmax semantics on non-finite logits: a NaN ranks first (the first NaN
