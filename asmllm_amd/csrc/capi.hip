@@ -521,6 +521,13 @@ extern "C" int asmhip_gemm_q8_0(const void* w_blocks, const void* a_blocks, floa
     return rc ? rc : gemm_q8_0_launch(w_blocks, a_blocks, c, T, M, K, (hipStream_t)stream);
 }
 
+extern "C" int asmhip_gemm_q8_split(const int8_t* w_qs, const float* w_scales, const int8_t* a_qs,
+                                    const float* a_scales, float* c, int64_t T, int64_t M, int64_t K, void* stream) {
+    int rc = check_ptrs(w_qs, a_qs, c);
+    if (!rc && (!w_scales || !a_scales)) rc = fail(kInvalidArgument, "null scales");
+    return rc ? rc : gemm_q8_split_launch(w_qs, w_scales, a_qs, a_scales, c, T, M, K, (hipStream_t)stream);
+}
+
 extern "C" int asmhip_set_q4_kernel(int kernel) { return set_q4_kernel(kernel); }
 extern "C" int asmhip_get_q4_kernel(void) { return get_q4_kernel(); }
 
@@ -529,6 +536,12 @@ extern "C" int asmhip_quantize(int qtype, const float* w, void* blocks, int64_t 
     if (!w || !blocks) return fail(kInvalidArgument, "null pointer argument");
     int rc = quant_type(qtype, &qt);
     return rc ? rc : quantize_launch(qt, w, blocks, rows, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_quantize_q8_split(const float* w, int8_t* qs, float* scales, int64_t rows, int64_t K,
+                                        void* stream) {
+    int rc = check_ptrs(w, qs, scales);
+    return rc ? rc : quantize_q8_split_launch(w, qs, scales, rows, K, (hipStream_t)stream);
 }
 
 extern "C" int asmhip_random_blocks(int qtype, void* blocks, int64_t rows, int64_t K, uint64_t seed, float stddev,

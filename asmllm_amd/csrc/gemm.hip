@@ -27,6 +27,8 @@
 // raw in LDS (row pitch an odd number of dwords: conflict-free operand reads),
 // double-buffered with the next step's loads in flight.  Other K: blocks are
 // staged one by one with qs realigned on the way into LDS.
+// gemm_q8_split takes the split operands of asm_matmul_q8 (int8 qs planes and
+// fp32 scale planes) with the same tiling; see its comment.
 #include <type_traits>
 
 #include "common.hpp"
@@ -386,6 +388,137 @@ __global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* _
     }
 }
 
+// ---------------------------------------------------------------------------
+// Split-layout variant: int8 qs planes [rows][K] and fp32 scale planes
+// [rows][K/32], the operand layout of the reference's asm_matmul_q8
+// (matmul_q8_avx2.asm:51-194: qweights int8[M][K/32][32], scales f32[M][K/32]).
+// A K step of two blocks is 64 contiguous qs bytes and 8 scale bytes per row.
+// qs rows are parked at an 80-byte pitch (five 16-byte units, an odd number:
+// each group of 8 lanes of a 32-row b128 operand read covers the 8 bank quads
+// once), so an operand is one aligned ds_read_b128 with no realignment.  The
+// scale product d_a d_w comes from v_mfma_f32_32x32x2_f32 with the scales in
+// k = 0 and zeros in k = 1: one fp32 product per output, rounded once, as the
+// CPU's fmul, for any fp32 scales.  The k = 1 lanes read their zeros from a
+// zero-filled copy of the scale area, so no per-block select is needed.
+// ---------------------------------------------------------------------------
+constexpr int kSplitThreads = 512;                              // 8 waves of one 32x32 tile
+constexpr int kSplitPitch = 80;                                 // qs bytes per staged row (64 used)
+constexpr int kSplitRows = kTT + kTM;                           // A rows, then W rows
+constexpr int kSplitScOff = kSplitRows * kSplitPitch;           // scales [g][row][2 blocks], g = 1 zeros
+constexpr int kSplitScHalf = kSplitRows * 2 * 4;
+constexpr int kSplitStage = kSplitScOff + 2 * kSplitScHalf;
+
+__global__ __launch_bounds__(kSplitThreads) void gemm_q8_split(const int8_t* __restrict__ wq,
+                                                               const float* __restrict__ wsc,
+                                                               const int8_t* __restrict__ aq,
+                                                               const float* __restrict__ asc,
+                                                               float* __restrict__ c, int T, int M, int K,
+                                                               int tiles_t, int n_tiles) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    // XCD-aware tile order, as in gemm_q8_0_coalesced
+    const int chunk = (int)gridDim.x >> 3;
+    const int tile = ((int)blockIdx.x & 7) * chunk + ((int)blockIdx.x >> 3);
+    if (tile >= n_tiles) return;
+    const int nb = K >> 5;
+    const int t0 = (tile % tiles_t) * kTT, j0 = (tile / tiles_t) * kTM;
+    const int tid = (int)threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wt = wave >> 2, wm = wave & 3;
+    const auto aqr = make_rsrc(aq, (uint32_t)T * (uint32_t)K);
+    const auto wqr = make_rsrc(wq, (uint32_t)M * (uint32_t)K);
+    const auto asr = make_rsrc(asc, (uint32_t)T * (uint32_t)nb * 4u);
+    const auto wsr = make_rsrc(wsc, (uint32_t)M * (uint32_t)nb * 4u);
+
+    // Staging roles (wave-uniform): piece q = (staged row q / 4, 16-byte piece
+    // q % 4) of the step's 768 qs pieces.  Slot 0: piece tid (waves 0-3: A
+    // rows, waves 4-7: W rows 0-63); slot 1 (waves 0-3): piece 512 + tid (W rows
+    // 64-127); waves 4-6 also fetch the 8 scale bytes of staged row tid - 256.
+    const bool two_qs = wave < 4, has_sc = wave >= 4 && wave < 7;
+    const bool sc_a = wave == 4;
+    const int r0 = tid >> 2, r1 = 128 + (tid >> 2), k4 = tid & 3;
+    const int rs = tid - 256;  // staged row of this thread's scales (waves 4-6)
+    auto grow_of = [&](int r) { return r < kTT ? t0 + r : j0 + (r - kTT); };
+    auto row_live = [&](int r) { return r < kTT ? t0 + r < T : j0 + (r - kTT) < M; };
+    const uint32_t q0 = row_live(r0) ? (uint32_t)grow_of(r0) * (uint32_t)K + 16u * k4 : kPastEnd;
+    const uint32_t q1 = two_qs && row_live(r1) ? (uint32_t)grow_of(r1) * (uint32_t)K + 16u * k4 : kPastEnd;
+    const uint32_t s0 = has_sc && row_live(rs) ? (uint32_t)grow_of(rs) * (uint32_t)nb * 4u : kPastEnd;
+    // a K step past the last block (K % 64 == 32): its second block's pieces load zeros
+    const bool hi_piece = k4 >= 2;
+
+    uint4 p0, p1;
+    uint2 ps;
+    auto fetch = [&](int kb0) {
+        const bool pair = kb0 + 1 < nb;  // wave-uniform
+        const uint32_t kq = (uint32_t)kb0 * 32u;
+        const uint32_t o0 = q0 == kPastEnd || (hi_piece && !pair) ? kPastEnd : q0 + kq;
+        p0 = buf_load_b128(two_qs ? aqr : wqr, o0);
+        if (two_qs) {
+            const uint32_t o1 = q1 == kPastEnd || (hi_piece && !pair) ? kPastEnd : q1 + kq;
+            p1 = buf_load_b128(wqr, o1);
+        }
+        if (has_sc) {
+            const uint32_t os = s0 == kPastEnd ? kPastEnd : s0 + (uint32_t)kb0 * 4u;
+            if (pair)
+                ps = buf_load_b64(sc_a ? asr : wsr, os);
+            else
+                ps = make_uint2(buf_load_b32(sc_a ? asr : wsr, os), 0u);
+        }
+    };
+    auto park = [&](uint8_t* stage) {
+        *reinterpret_cast<uint4*>(stage + r0 * kSplitPitch + 16 * k4) = p0;
+        if (two_qs) *reinterpret_cast<uint4*>(stage + r1 * kSplitPitch + 16 * k4) = p1;
+        if (has_sc) *reinterpret_cast<uint2*>(stage + kSplitScOff + rs * 8) = ps;
+    };
+    // the k = 1 half of both stages' scale areas: zeros, written once
+    for (int i = tid; i < 2 * kSplitScHalf / 4; i += kSplitThreads) {
+        const int st = i / (kSplitScHalf / 4), e = i - st * (kSplitScHalf / 4);
+        reinterpret_cast<float*>(lds + st * kSplitStage + kSplitScOff + kSplitScHalf)[e] = 0.f;
+    }
+
+    const int m = lane & 31, g = lane >> 5;
+    const int arow = 32 * wt + m, wrow = kTT + 32 * wm + m;
+    const int a_qs = arow * kSplitPitch + 16 * g, w_qs = wrow * kSplitPitch + 16 * g;
+    const int a_sc = kSplitScOff + g * kSplitScHalf + arow * 8, w_sc = kSplitScOff + g * kSplitScHalf + wrow * 8;
+    v16f acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+
+    const int nsteps = (nb + 1) >> 1;
+    fetch(0);
+    for (int s = 0; s < nsteps; ++s) {
+        uint8_t* stage = lds + (s & 1) * kSplitStage;
+        park(stage);
+        __syncthreads();
+        if (s + 1 < nsteps) fetch(2 * (s + 1));
+        const bool pair = 2 * s + 1 < nb;  // false only in the last step of an odd block count
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+            if (blk == 1 && !pair) break;  // no block: nothing is added (not even a zero)
+            const v4i av = *reinterpret_cast<const v4i*>(stage + a_qs + 32 * blk);
+            const v4i bv = *reinterpret_cast<const v4i*>(stage + w_qs + 32 * blk);
+            const float da = *reinterpret_cast<const float*>(stage + a_sc + 4 * blk);
+            const float dw = *reinterpret_cast<const float*>(stage + w_sc + 4 * blk);
+            __builtin_amdgcn_sched_barrier(0);
+            const v16i zi = {};
+            const v16f zf = {};
+            const v16i dd = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zi, 0, 0, 0);
+            const v16f ss = __builtin_amdgcn_mfma_f32_32x32x2f32(da, dw, zf, 0, 0, 0);  // d_a d_w
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = fmaf((float)dd[i], ss[i], acc[i]);
+        }
+    }
+
+    const int col = j0 + 32 * wm + m;
+    if (col < M) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = t0 + 32 * wt + 8 * (i / 4) + 4 * g + i % 4;
+            if (row < T) c[(size_t)row * M + col] = acc[i];
+        }
+    }
+}
+
 // Two blocks per staged K step, one step of loads in flight per thread.
 // Deeper register rings (2-4 steps) and 4- or 8-block steps measured slower on
 // MI355X: the extra registers cost occupancy.  So did issuing both blocks'
@@ -425,6 +558,27 @@ int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t 
         hipLaunchKernelGGL((gemm_q8_0_kernel<kKB, false>), grid, dim3(kThreadsG), lds, st,
                            static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(a), c, (int)T, (int)M, (int)K);
     }
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int gemm_q8_split_launch(const int8_t* wq, const float* wsc, const int8_t* aq, const float* asc, float* c, int64_t T,
+                         int64_t M, int64_t K, hipStream_t st) {
+    if (T <= 0 || M <= 0 || K <= 0 || K % 32)
+        return fail(kInvalidArgument, "gemm_split: need T, M, K > 0 and K %% 32 == 0 (got T=%lld M=%lld K=%lld)",
+                    (long long)T, (long long)M, (long long)K);
+    if ((T + kTT) * K >= (int64_t)kPastEnd || (M + kTM) * K >= (int64_t)kPastEnd)
+        return fail(kInvalidArgument, "gemm_split: operands above 4 GB are not supported");
+    if ((uintptr_t)wq % 16 || (uintptr_t)aq % 16 || (uintptr_t)wsc % 4 || (uintptr_t)asc % 4)
+        return fail(kInvalidArgument, "gemm_split: qs planes must be 16-byte aligned, scales 4-byte aligned");
+    const int64_t tiles_t = (T + kTT - 1) / kTT, n_tiles = tiles_t * ((M + kTM - 1) / kTM);
+    if (n_tiles > (1 << 24)) return fail(kInvalidArgument, "gemm_split: T x M too large");
+    const unsigned padded = (unsigned)((n_tiles + 7) / 8 * 8);
+    const size_t lds = 2 * (size_t)kSplitStage;
+    const int rc = dynamic_lds((const void*)gemm_q8_split, lds);
+    if (rc) return rc;
+    hipLaunchKernelGGL(gemm_q8_split, dim3(padded), dim3(kSplitThreads), lds, st, wq, wsc, aq, asc, c, (int)T, (int)M,
+                       (int)K, (int)tiles_t, (int)n_tiles);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

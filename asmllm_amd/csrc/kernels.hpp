@@ -83,6 +83,8 @@ int split_mfma_launch(int bits, const void* qs, const uint8_t* qh, const float* 
 // C[T][M] = A (Q8_0 blocks [T][K/32]) x W (Q8_0 blocks [M][K/32])^T, block dots
 // scaled by both fp16 scales and accumulated in block order.
 int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t M, int64_t K, hipStream_t stream);
+int gemm_q8_split_launch(const int8_t* wq, const float* wsc, const int8_t* aq, const float* asc, float* c, int64_t T,
+                         int64_t M, int64_t K, hipStream_t stream);
 
 // Plain streaming read of `bytes` in one launch (measurement: the single-launch
 // read floor); `sink` is 4 KB of device memory the kernel practically never writes.
@@ -93,6 +95,7 @@ int dequant_launch(QuantType qt, const void* w, float* out, int64_t rows, int64_
 
 // fp32 [rows][K] -> GGUF blocks (the rules of the host quantizers, bit for bit).
 int quantize_launch(QuantType qt, const float* w, void* blocks, int64_t rows, int64_t K, hipStream_t stream);
+int quantize_q8_split_launch(const float* w, int8_t* qs, float* scales, int64_t rows, int64_t K, hipStream_t stream);
 // Q4_0 / Q8_0 blocks of N(0, stddev^2) weights from a counter-based generator.
 int random_blocks_launch(QuantType qt, void* blocks, int64_t rows, int64_t K, uint64_t seed, float stddev,
                          hipStream_t stream);

@@ -54,22 +54,30 @@ __device__ __forceinline__ void quant_q4_block(const float* v, uint8_t* out) {
     }
 }
 
-__device__ __forceinline__ void quant_q8_block(const float* v, uint8_t* out) {
+// The Q8_0 rules for one block: the 32 quants into q, the fp16 d's bits returned.
+__device__ __forceinline__ unsigned short quant_q8_values(const float* v, int8_t* q) {
 #pragma clang fp contract(off)
     float amax = 0.f;
 #pragma unroll
     for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
     const float d = amax / 127.0f;
     const float inv = amax == 0.0f ? 0.0f : 127.0f / amax;
-    const unsigned short dh = __half_as_ushort(__float2half_rn(d));
-    out[0] = (uint8_t)(dh & 0xFF);
-    out[1] = (uint8_t)(dh >> 8);
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
         float r = rintf(v[j] * inv);
         r = fminf(fmaxf(r, -128.0f), 127.0f);
-        out[2 + j] = (uint8_t)(int8_t)(int)r;
+        q[j] = (int8_t)(int)r;
     }
+    return __half_as_ushort(__float2half_rn(d));
+}
+
+__device__ __forceinline__ void quant_q8_block(const float* v, uint8_t* out) {
+    int8_t q[32];
+    const unsigned short dh = quant_q8_values(v, q);
+    out[0] = (uint8_t)(dh & 0xFF);
+    out[1] = (uint8_t)(dh >> 8);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) out[2 + j] = (uint8_t)q[j];
 }
 
 template <bool kQ8>
@@ -84,6 +92,26 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(const float* __restr
         quant_q8_block(v, out + i * 34);
     else
         quant_q4_block(v, out + i * 18);
+}
+
+// The split layout of the same blocks: qs[i] = the 32 quants of block i
+// (16-byte aligned), scales[i] = its fp16 d widened to fp32.
+__global__ __launch_bounds__(kThreads) void quantize_q8_split_kernel(const float* __restrict__ w, int8_t* __restrict__ qs,
+                                                                     float* __restrict__ scales, int64_t nblocks) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= nblocks) return;
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = w[i * 32 + j];
+    union {
+        int8_t b[32];
+        uint4 u[2];
+    } q;
+    const unsigned short dh = quant_q8_values(v, q.b);
+    uint4* dst = reinterpret_cast<uint4*>(qs + i * 32);
+    dst[0] = q.u[0];
+    dst[1] = q.u[1];
+    scales[i] = __half2float(__ushort_as_half(dh));
 }
 
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
@@ -152,6 +180,16 @@ int quantize_launch(QuantType qt, const float* w, void* blocks, int64_t rows, in
     else
         hipLaunchKernelGGL((quantize_kernel<true>), dim3((unsigned)grid_for(nb)), dim3(kThreads), 0, st, w,
                            (uint8_t*)blocks, nb);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int quantize_q8_split_launch(const float* w, int8_t* qs, float* scales, int64_t rows, int64_t K, hipStream_t st) {
+    if (rows <= 0 || K <= 0 || K % 32) return fail(kInvalidArgument, "quantize_q8_split: need rows > 0 and K %% 32 == 0");
+    if ((uintptr_t)qs % 16) return fail(kInvalidArgument, "quantize_q8_split: qs must be 16-byte aligned");
+    const int64_t nb = rows * (K / 32);
+    if (grid_for(nb) > INT32_MAX) return fail(kInvalidArgument, "quantize_q8_split: tensor too large");
+    hipLaunchKernelGGL(quantize_q8_split_kernel, dim3((unsigned)grid_for(nb)), dim3(kThreads), 0, st, w, qs, scales, nb);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

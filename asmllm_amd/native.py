@@ -58,9 +58,11 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_matmul_fused": (c_int, [c_int, _P, _P, _P, c_int64, c_int64, c_int, _P, c_float, c_int, _P]),
     "asmhip_matmul_swiglu": (c_int, [c_int, _P, _P, _P, c_int64, c_int64, c_int, _P, c_float, _P, _P]),
     "asmhip_gemm_q8_0": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, _P]),
+    "asmhip_gemm_q8_split": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P]),
     "asmhip_set_q4_kernel": (c_int, [c_int]),
     "asmhip_get_q4_kernel": (c_int, []),
     "asmhip_quantize": (c_int, [c_int, _P, _P, c_int64, c_int64, _P]),
+    "asmhip_quantize_q8_split": (c_int, [_P, _P, _P, c_int64, c_int64, _P]),
     "asmhip_random_blocks": (c_int, [c_int, _P, c_int64, c_int64, c_uint64, c_float, _P]),
     "asmhip_random_f16": (c_int, [_P, c_int64, c_uint64, c_float, _P]),
     "asmhip_fill_f32": (c_int, [_P, c_int64, c_float, _P]),

@@ -614,10 +614,36 @@ def bench_gemm(T: int = 512, M: int = 11008, K: int = 4096, copies: int = 12) ->
     ops = 2 * T * M * K
     nbytes = gguf.q8_0_nbytes(M, K) + gguf.q8_0_nbytes(T, K) + 4 * T * M
     log(f"GEMM {T}x{M}x{K}: {us:.2f} us, {ops / us / 1e6:.0f} TOP/s")
+
+    # the same operands in the split layout (int8 qs planes + fp32 scale planes);
+    # the results are bitwise those of the block-form GEMM
+    nb = K // 32
+    w0 = wbufs[0].download(np.uint8, (M, nb, 34))
+    wq = DeviceBuffer.from_numpy(np.ascontiguousarray(w0[:, :, 2:]).view(np.int8))
+    ws = DeviceBuffer.from_numpy(w0[:, :, 0:2].copy().view(np.float16).reshape(M, nb).astype(np.float32))
+    wsplit = [(wq, ws)] + [(DeviceBuffer(wq.nbytes), DeviceBuffer(ws.nbytes)) for _ in range(copies - 1)]
+    for q, s in wsplit[1:]:
+        q.copy_from(wq)
+        s.copy_from(ws)
+    a0 = dq.download(np.uint8, (T, nb, 34))  # the same activation blocks
+    aq = DeviceBuffer.from_numpy(np.ascontiguousarray(a0[:, :, 2:]).view(np.int8))
+    as_ = DeviceBuffer.from_numpy(a0[:, :, 0:2].copy().view(np.float16).reshape(T, nb).astype(np.float32))
+
+    def gemm_split(i, st):
+        q, s = wsplit[i % copies]
+        native.check(lib.asmhip_gemm_q8_split(q.ptr, s.ptr, aq.ptr, as_.ptr, dc.ptr, T, M, K, st), "gemm split")
+
+    us_s = time_launches(gemm_split, copies, reps=20)
+    nbytes_s = M * K + 4 * M * nb + T * K + 4 * T * nb + 4 * T * M
+    log(f"GEMM split layout: {us_s:.2f} us, {ops / us_s / 1e6:.0f} TOP/s")
     return {"workload": f"Q8_0 GEMM C[{T}][{M}] = A_q8[{T}][{K}] . W_q8[{M}][{K}]^T", "us": round(us, 3),
             "TOPs": round(ops / us / 1e6, 1), "frac_int8_mfma_peak": round(ops / us / 1e6 / INT8_MFMA_PEAK_TOPS, 4),
             "GBps": round(nbytes / us / 1e3, 1), "activation_quantize_us": round(us_q, 3), "ops": ops,
-            "bytes": nbytes}
+            "bytes": nbytes,
+            "split_layout": {"layout": "int8 qs [rows][K] + fp32 scales [rows][K/32] (asm_matmul_q8's operands)",
+                             "us": round(us_s, 3), "TOPs": round(ops / us_s / 1e6, 1),
+                             "frac_int8_mfma_peak": round(ops / us_s / 1e6 / INT8_MFMA_PEAK_TOPS, 4),
+                             "bytes": nbytes_s}}
 
 
 def decode_cpu_baseline(eng, context: int, seconds: float) -> dict:

@@ -177,6 +177,14 @@ ASMHIP_API int asmhip_matmul_swiglu(int qtype, const void* blocks, const float* 
  * applied to a batch; the reference itself has no GEMM. */
 ASMHIP_API int asmhip_gemm_q8_0(const void* w_blocks, const void* a_blocks, float* c, int64_t T, int64_t M,
                                 int64_t K, void* stream);
+/* The same GEMM on the split layout of asm_matmul_q8 (matmul_q8_avx2.asm:51-194): int8 qs
+ * planes [rows][K] (16-byte aligned) and fp32 scale planes [rows][K/32], for W (M rows) and A
+ * (T rows; quantize activations with asmhip_quantize_q8_split).  Per block the scale is the
+ * fp32 product d_w * d_a (any fp32 scales), then acc = fmaf(float(dot), scale, acc) in block
+ * order: with scales widened from fp16 the result is bitwise that of asmhip_gemm_q8_0 on the
+ * same blocks. */
+ASMHIP_API int asmhip_gemm_q8_split(const int8_t* w_qs, const float* w_scales, const int8_t* a_qs,
+                                    const float* a_scales, float* c, int64_t T, int64_t M, int64_t K, void* stream);
 /* Process-wide Q4_0 GGUF kernel choice (ASMHIP_Q4_KERNEL_*). */
 ASMHIP_API int asmhip_set_q4_kernel(int kernel);
 ASMHIP_API int asmhip_get_q4_kernel(void);
@@ -186,6 +194,10 @@ ASMHIP_API int asmhip_get_q4_kernel(void);
  * q = round-half-even(w * 127 / amax) saturated (matmul_q4_neon.S:80-135);
  * d stored as fp16 (round to nearest even). */
 ASMHIP_API int asmhip_quantize(int qtype, const float* w, void* blocks, int64_t rows, int64_t K, void* stream);
+/* Q8_0 quantization as above into the split layout: qs[rows][K] int8 (16-byte aligned) and
+ * scales[rows][K/32] = the fp16 d widened to fp32 (the operands of asmhip_gemm_q8_split). */
+ASMHIP_API int asmhip_quantize_q8_split(const float* w, int8_t* qs, float* scales, int64_t rows, int64_t K,
+                                        void* stream);
 /* Synthetic model data generated in HBM: blocks of N(0, stddev^2) weights
  * quantized as above, fp16 N(0, stddev^2) values, or a constant fill. */
 ASMHIP_API int asmhip_random_blocks(int qtype, void* blocks, int64_t rows, int64_t K, uint64_t seed, float stddev,

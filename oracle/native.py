@@ -43,6 +43,7 @@ _SIGS = {
     "oracle_matmul_q8_mt": (None, [_P, _P, _P, _P, c_int64, c_int64, c_int]),
     "oracle_threadpool_dispatch_q8": (None, [_P, _P, _P, _P, c_int64, c_int64]),
     "oracle_gemm_q8_0": (None, [_P, _P, _P, c_int64, c_int64, c_int64, c_int]),
+    "oracle_gemm_q8_split": (None, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int]),
     "oracle_rmsnorm": (None, [_P, _P, _P, c_int64, c_float]),
     "oracle_rope": (None, [_P, _P, c_int64, c_int64, c_float]),
     "oracle_softmax": (None, [_P, _P, c_int64]),
@@ -246,6 +247,17 @@ def gemm_q8_0(w_blocks, a_blocks, nt: int = 1) -> np.ndarray:
     M, T, K = w.shape[0], a.shape[0], w.shape[1] * 32
     c = np.zeros((T, M), np.float32)
     lib().oracle_gemm_q8_0(_ptr(w), _ptr(a), _ptr(c), T, M, K, nt)
+    return c
+
+
+def gemm_q8_split(w_qs, w_scales, a_qs, a_scales, nt: int = 1) -> np.ndarray:
+    """Split operands: qs int8 [rows][K/32][32] (or [rows][K]), scales fp32 [rows][K/32]."""
+    wq, aq = _c(w_qs, np.int8), _c(a_qs, np.int8)
+    ws, as_ = _c(w_scales, np.float32), _c(a_scales, np.float32)
+    M, T = wq.shape[0], aq.shape[0]
+    K = wq.size // M
+    c = np.zeros((T, M), np.float32)
+    lib().oracle_gemm_q8_split(_ptr(wq), _ptr(ws), _ptr(aq), _ptr(as_), _ptr(c), T, M, K, nt)
     return c
 
 

@@ -876,6 +876,54 @@ void oracle_gemm_q8_0(const uint8_t* w_blocks, const uint8_t* a_blocks, float* c
     pool_run(gemm_job_run, &g);
 }
 
+/* The same recipe on the split layout of asm_matmul_q8 (matmul_q8_avx2.asm:51-194):
+ * int8 qs [rows][K] and fp32 scales [rows][K/32]; the scale is the fp32 product
+ * w_scale * x_scale, as matmul_q4_neon.S:190-255 forms it. */
+typedef struct {
+    const int8_t *wq, *aq;
+    const float *ws, *as;
+    float* c;
+    int64_t T, M, K;
+} gemm_split_job;
+
+static void gemm_split_rows(const gemm_split_job* g, int64_t t0, int64_t t1) {
+    int64_t nb = g->K / 32;
+    for (int64_t t = t0; t < t1; ++t) {
+        for (int64_t j = 0; j < g->M; ++j) {
+            float acc = 0.0f;
+            for (int64_t b = 0; b < nb; ++b) {
+                const int8_t* qa = g->aq + (t * nb + b) * 32;
+                const int8_t* qw = g->wq + (j * nb + b) * 32;
+                int32_t dot = 0;
+                for (int k = 0; k < 32; ++k) dot += (int32_t)qa[k] * (int32_t)qw[k]; /* sdot */
+                float sc = g->ws[j * nb + b] * g->as[t * nb + b];                    /* fmul */
+                acc = fmaf((float)dot, sc, acc);                                     /* scvtf, fmadd */
+            }
+            g->c[t * g->M + j] = acc;
+        }
+    }
+}
+
+static void gemm_split_job_run(void* ctx, int i, int nt) {
+    gemm_split_job* g = (gemm_split_job*)ctx;
+    int64_t per = (g->T + nt - 1) / nt;
+    int64_t t0 = (int64_t)i * per, t1 = t0 + per;
+    if (t0 > g->T) t0 = g->T;
+    if (t1 > g->T) t1 = g->T;
+    if (t1 > t0) gemm_split_rows(g, t0, t1);
+}
+
+void oracle_gemm_q8_split(const int8_t* w_qs, const float* w_scales, const int8_t* a_qs, const float* a_scales,
+                          float* c, int64_t T, int64_t M, int64_t K, int nt) {
+    gemm_split_job g = {w_qs, a_qs, w_scales, a_scales, c, T, M, K};
+    if (nt <= 1 || T < 2) {
+        gemm_split_rows(&g, 0, T);
+        return;
+    }
+    if (g_pool_size != nt) oracle_threadpool_init(nt);
+    pool_run(gemm_split_job_run, &g);
+}
+
 /* ======================================================================== */
 /* a9: decode-step ops                                                       */
 /* ======================================================================== */

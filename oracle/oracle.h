@@ -121,6 +121,10 @@ ORACLE_API void oracle_threadpool_dispatch_q8(const int8_t* qweights, const floa
  * the two scales, fmadd).  nt > 1 splits over rows of C. */
 ORACLE_API void oracle_gemm_q8_0(const uint8_t* w_blocks, const uint8_t* a_blocks, float* c,
                                  int64_t T, int64_t M, int64_t K, int nt);
+/* The same GEMM on split operands: int8 qs [rows][K], fp32 scales [rows][K/32]
+ * (scale = w_scale * a_scale in fp32, then fmaf in block order). */
+ORACLE_API void oracle_gemm_q8_split(const int8_t* w_qs, const float* w_scales, const int8_t* a_qs,
+                                     const float* a_scales, float* c, int64_t T, int64_t M, int64_t K, int nt);
 
 /* ---- a9: decode-step ops -------------------------------------------------- */
 

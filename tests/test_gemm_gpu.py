@@ -115,3 +115,107 @@ def test_gemm_rejects_bad_arguments(hip):
     assert hip.asmhip_gemm_q8_0(d.ptr, d.ptr, d.ptr, 4, 4, 40, None) == native.ERR_INVALID_ARGUMENT
     assert hip.asmhip_gemm_q8_0(d.ptr, d.ptr, d.ptr, 0, 4, 32, None) == native.ERR_INVALID_ARGUMENT
     assert hip.asmhip_gemm_q8_0(None, d.ptr, d.ptr, 4, 4, 32, None) == native.ERR_INVALID_ARGUMENT
+
+
+# ---- split layout: int8 qs planes + fp32 scale planes (asm_matmul_q8's operands) ----------
+
+def _gemm_split(hip, wq, ws, aq, as_):
+    M, T = wq.shape[0], aq.shape[0]
+    K = wq.size // M
+    bufs = [DeviceBuffer.from_numpy(np.ascontiguousarray(v)) for v in (wq, ws, aq, as_)]
+    dc = DeviceBuffer(T * M * 4)
+    rc = hip.asmhip_gemm_q8_split(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, dc.ptr, T, M, K, None)
+    assert rc == 0, hip.asmhip_last_error()
+    synchronize()
+    return dc.download(np.float32, (T, M))
+
+
+@pytest.mark.parametrize("T,M,K", [(64, 128, 128), (512, 11008, 4096), (1, 1, 32), (7, 31, 96), (33, 200, 160),
+                                   (100, 129, 4096), (65, 257, 224)])
+def test_gemm_split_matches_block_gemm_and_oracle(hip, oracle, T, M, K):
+    """Scales widened from fp16: bitwise the block-form GEMM on the same blocks, and
+    bitwise the oracle (all rows at the small shapes, 8 rows of the 512-row one)."""
+    w_blocks, a_blocks = _problem(T * 7 + M + K + 1, T, M, K)
+    wq, ws = oracle.split_q8_0(w_blocks)
+    aq, as_ = oracle.split_q8_0(a_blocks)
+    c = _gemm_split(hip, wq, ws, aq, as_)
+    np.testing.assert_array_equal(c, _gemm(hip, w_blocks, a_blocks))
+    rows = slice(0, min(T, 8)) if T * M * K > 1e9 else slice(0, T)
+    np.testing.assert_array_equal(c[rows], oracle.gemm_q8_split(wq, ws, aq[rows], as_[rows], NT))
+
+
+def test_gemm_split_arbitrary_fp32_scales(hip, oracle):
+    """fp32 scales that no fp16 holds (U(0.5, 1.5), times 2^-30..2^30 on the
+    activations): each block's scale is the fp32 product, rounded once, as the
+    oracle's fmul; outputs bitwise the oracle's."""
+    rng = np.random.default_rng(21)
+    T, M, K = 96, 256, 1056
+    nb = K // 32
+    wq = rng.integers(-128, 128, (M, nb, 32)).astype(np.int8)
+    aq = rng.integers(-128, 128, (T, nb, 32)).astype(np.int8)
+    ws = rng.uniform(0.5, 1.5, (M, nb)).astype(np.float32)
+    as_ = (rng.uniform(0.5, 1.5, (T, nb)) * 2.0 ** rng.integers(-30, 30, (T, nb))).astype(np.float32)
+    np.testing.assert_array_equal(_gemm_split(hip, wq, ws, aq, as_), oracle.gemm_q8_split(wq, ws, aq, as_, NT))
+
+
+def test_gemm_split_subnormal_scale_products(hip, oracle):
+    """Scale products below the fp32 normal range (2^-140, 2^-145) and outputs that
+    are subnormal or just normal: the matrix pipe keeps them, bitwise the oracle's."""
+    rng = np.random.default_rng(25)
+    T, M, K = 64, 160, 256
+    nb = K // 32
+    wq = rng.integers(-128, 128, (M, nb, 32)).astype(np.int8)
+    aq = rng.integers(-128, 128, (T, nb, 32)).astype(np.int8)
+    ws = (2.0 ** rng.integers(-75, -60, (M, nb)) * rng.uniform(1, 2, (M, nb))).astype(np.float32)
+    as_ = (2.0 ** rng.integers(-75, -60, (T, nb)) * rng.uniform(1, 2, (T, nb))).astype(np.float32)
+    assert np.any(ws[None, :, :] * as_[:, None, :] < np.finfo(np.float32).tiny)
+    np.testing.assert_array_equal(_gemm_split(hip, wq, ws, aq, as_), oracle.gemm_q8_split(wq, ws, aq, as_, NT))
+
+
+def test_quantize_q8_split_matches_block_quantizer(hip, oracle):
+    """The split-output quantizer writes the block quantizer's quants and its fp16 d
+    widened to fp32 (an all-zero row and large values included)."""
+    rng = np.random.default_rng(22)
+    T, K = 37, 4128
+    a = rng.standard_normal((T, K)).astype(np.float32)
+    a[3] = 0.0
+    a[5, :64] *= 1e4
+    da, db = DeviceBuffer.from_numpy(a), DeviceBuffer(gguf.q8_0_nbytes(T, K))
+    dq, ds = DeviceBuffer(T * K), DeviceBuffer(T * K // 32 * 4)
+    assert hip.asmhip_quantize_q8_split(da.ptr, dq.ptr, ds.ptr, T, K, None) == 0, hip.asmhip_last_error()
+    assert hip.asmhip_quantize(native.Q8_0, da.ptr, db.ptr, T, K, None) == 0, hip.asmhip_last_error()
+    synchronize()
+    blocks = db.download(np.uint8, (T, K // 32, 34))
+    np.testing.assert_array_equal(blocks, oracle.quantize_q8_0(a))
+    qs_ref, sc_ref = oracle.split_q8_0(blocks)
+    np.testing.assert_array_equal(dq.download(np.int8, (T, K // 32, 32)), qs_ref)
+    np.testing.assert_array_equal(ds.download(np.float32, (T, K // 32)), sc_ref)
+
+
+def test_gemm_split_from_fp32_activations(hip, oracle):
+    """fp32 activations -> split quantizer -> split GEMM, bitwise the block path."""
+    T, M, K = 96, 384, 1024
+    rng = np.random.default_rng(23)
+    a = rng.standard_normal((T, K)).astype(np.float32)
+    w_blocks, _ = _problem(24, 1, M, K)
+    wq, ws = oracle.split_q8_0(w_blocks)
+    da = DeviceBuffer.from_numpy(a)
+    dq, ds = DeviceBuffer(T * K), DeviceBuffer(T * K // 32 * 4)
+    dwq, dws, dc = DeviceBuffer.from_numpy(wq), DeviceBuffer.from_numpy(ws), DeviceBuffer(T * M * 4)
+    assert hip.asmhip_quantize_q8_split(da.ptr, dq.ptr, ds.ptr, T, K, None) == 0
+    assert hip.asmhip_gemm_q8_split(dwq.ptr, dws.ptr, dq.ptr, ds.ptr, dc.ptr, T, M, K, None) == 0
+    synchronize()
+    a_blocks = oracle.quantize_q8_0(a)
+    np.testing.assert_array_equal(dc.download(np.float32, (T, M)), oracle.gemm_q8_0(w_blocks, a_blocks, NT))
+
+
+def test_gemm_split_rejects_bad_arguments(hip):
+    d = DeviceBuffer(1 << 16)
+    p = d.ptr
+    bad = native.ERR_INVALID_ARGUMENT
+    assert hip.asmhip_gemm_q8_split(p, p, p, p, p, 4, 4, 40, None) == bad      # K % 32
+    assert hip.asmhip_gemm_q8_split(p, p, p, p, p, 0, 4, 32, None) == bad      # T = 0
+    assert hip.asmhip_gemm_q8_split(p + 4, p, p, p, p, 4, 4, 32, None) == bad  # qs not 16-byte aligned
+    assert hip.asmhip_gemm_q8_split(p, None, p, p, p, 4, 4, 32, None) == bad
+    assert hip.asmhip_quantize_q8_split(p, p + 8, p, 4, 32, None) == bad
+    assert hip.asmhip_quantize_q8_split(p, p, p, 4, 40, None) == bad

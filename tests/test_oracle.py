@@ -273,6 +273,64 @@ def test_gemm_against_exact_integer_form(oracle):
     np.testing.assert_array_equal(oracle.gemm_q8_0(wb, ab, nt=3), c)
 
 
+def test_gemm_split_equals_block_form_on_widened_scales(oracle):
+    """With scales widened from the blocks' fp16 d, the split-operand GEMM is the
+    block-form GEMM bit for bit (the same products, roundings and order)."""
+    rng = np.random.default_rng(15)
+    T, M, K = 9, 13, 320
+    wb = oracle.quantize_q8_0((rng.standard_normal((M, K)) * 0.02).astype(np.float32))
+    ab = oracle.quantize_q8_0(rng.standard_normal((T, K)).astype(np.float32))
+    wq, ws = oracle.split_q8_0(wb)
+    aq, as_ = oracle.split_q8_0(ab)
+    c = oracle.gemm_q8_split(wq, ws, aq, as_)
+    np.testing.assert_array_equal(c, oracle.gemm_q8_0(wb, ab))
+    np.testing.assert_array_equal(oracle.gemm_q8_split(wq, ws, aq, as_, nt=4), c)
+
+
+def _round_f32(fr):
+    """The fp32 value nearest the rational fr, ties to even (no double rounding)."""
+    from fractions import Fraction
+
+    f = np.float32(float(fr))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    return min(cands, key=lambda v: (abs(Fraction(float(v)) - fr), int(np.float32(v).view(np.uint32)) & 1))
+
+
+def _gemm_split_exact_steps(wq, ws, aq, as_):
+    """Brute force in exact rationals: per block the fp32 product of the two
+    scales, then acc = round_f32(dot * scale + acc) in block order."""
+    from fractions import Fraction
+
+    T, M, nb = aq.shape[0], wq.shape[0], ws.shape[1]
+    c = np.zeros((T, M), np.float32)
+    for t in range(T):
+        for j in range(M):
+            acc = np.float32(0)
+            for b in range(nb):
+                dot = int(np.dot(aq[t, b].astype(np.int64), wq[j, b].astype(np.int64)))
+                sc = _round_f32(Fraction(float(ws[j, b])) * Fraction(float(as_[t, b])))
+                acc = _round_f32(Fraction(dot) * Fraction(float(sc)) + Fraction(float(acc)))
+            c[t, j] = acc
+    return c
+
+
+def test_gemm_split_matches_exact_rounding_brute_force(oracle):
+    """Arbitrary fp32 scales (U(0.5, 1.5) as the reference's tests draw them, and
+    wide exponents): every output equals the exact-rational evaluation of the
+    recipe's roundings; a plausible slip, the scales of one block taken from the
+    next, fails the same comparison."""
+    rng = np.random.default_rng(16)
+    T, M, nb = 3, 5, 4
+    wq = rng.integers(-128, 128, (M, nb, 32)).astype(np.int8)
+    aq = rng.integers(-128, 128, (T, nb, 32)).astype(np.int8)
+    ws = rng.uniform(0.5, 1.5, (M, nb)).astype(np.float32)
+    as_ = (rng.uniform(0.5, 1.5, (T, nb)) * 2.0 ** rng.integers(-40, 40, (T, nb))).astype(np.float32)
+    exact = _gemm_split_exact_steps(wq, ws, aq, as_)
+    np.testing.assert_array_equal(oracle.gemm_q8_split(wq, ws, aq, as_), exact)
+    slipped = oracle.gemm_q8_split(wq, np.roll(ws, 1, axis=1), aq, as_)
+    assert not np.array_equal(slipped, exact)
+
+
 # ---- decode attention over fp16 KV -----------------------------------------------------------
 
 def test_attention_decode_f16_against_numpy(oracle):
