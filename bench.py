@@ -488,11 +488,58 @@ def bench_matvec_table(min_rotated_bytes: int = 600_000_000) -> list[dict]:
         for b in bufs:
             b.close()
         log(f"{name}: {us:.3f} us, {algo / us / 1e3:.0f} GB/s")
-    layer = [r for r in rows if r["op"].startswith("llama3")]
+    layer = [r for r in rows if r["op"].startswith("llama3 ")]
     us = sum(r["us"] for r in layer)
     nbytes = sum(r["bytes"] for r in layer)
     rows.append({"op": "llama3 layer (7 matvecs)", "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1),
                  "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4), "bytes": nbytes})
+
+    # The same layer's matvecs as the decode engine launches them (asmllm_amd/engine.py):
+    # q/k/v stacked into one matrix with the attention RMSNorm fused into its read of x,
+    # o with the residual add, gate/up interleaved into one matrix with the FFN RMSNorm
+    # and SwiGLU fused (h = silu(gate) * up), down with the residual add: 4 launches.
+    d, ffn, kv = 4096, 14336, 1024
+    norm = DeviceBuffer(4 * ffn)
+    native.check(lib.asmhip_fill_f32(norm.ptr, ffn, 1.0, None), "fill")
+    hx, hh, work = DeviceBuffer(4 * ffn), DeviceBuffer(4 * ffn), DeviceBuffer(8 * ffn)
+    native.check(lib.asmhip_fill_f32(hx.ptr, ffn, 0.5, None), "fill")
+    native.check(lib.asmhip_fill_f32(hh.ptr, ffn, 0.5, None), "fill")
+    eps = 1e-5
+    engine_ops = [
+        ("llama3.engine q/k/v stacked 6144x4096 (RMSNorm)", d + 2 * kv, d,
+         lambda w, st, M, K: lib.asmhip_matmul_fused(native.Q4_0, w, hx.ptr, work.ptr, M, K, native.PRE_RMSNORM,
+                                                     norm.ptr, eps, 0, st)),
+        ("llama3.engine o 4096x4096 (residual add)", d, d,
+         lambda w, st, M, K: lib.asmhip_matmul_fused(native.Q4_0, w, hh.ptr, hx.ptr, M, K, native.PRE_NONE,
+                                                     None, eps, 1, st)),
+        ("llama3.engine gate/up 28672x4096 (RMSNorm, SwiGLU)", 2 * ffn, d,
+         lambda w, st, M, K: lib.asmhip_matmul_swiglu(native.Q4_0, w, hx.ptr, hh.ptr, M // 2, K, native.PRE_RMSNORM,
+                                                      norm.ptr, eps, work.ptr, st)),
+        ("llama3.engine down 4096x14336 (residual add)", d, ffn,
+         lambda w, st, M, K: lib.asmhip_matmul_fused(native.Q4_0, w, hh.ptr, hx.ptr, M, K, native.PRE_NONE,
+                                                     None, eps, 1, st)),
+    ]
+    eng_rows = []
+    for name, M, K, call in engine_ops:
+        copies = max(8, -(-min_rotated_bytes // (M * (K // 32) * 18)))
+        bufs, _ = _rotating_blocks(native.Q4_0, M, K, copies, seed=M * 5 + K)
+
+        def enqueue(i, st, bufs=bufs, M=M, K=K, name=name, call=call):
+            native.check(call(bufs[i % len(bufs)].ptr, st, M, K), name)
+
+        us = time_launches(enqueue, copies, reps=max(4, 4000 // copies))
+        algo = M * (K // 32) * 18 + 4 * K + 4 * M
+        eng_rows.append({"op": name, "us": round(us, 3), "GBps": round(algo / us / 1e3, 1),
+                         "frac": round(algo / us / 1e3 / HBM_PEAK_GBPS, 4), "bytes": algo})
+        for b in bufs:
+            b.close()
+        log(f"{name}: {us:.3f} us, {algo / us / 1e3:.0f} GB/s")
+    rows += eng_rows
+    us = sum(r["us"] for r in eng_rows)
+    nbytes = sum(r["bytes"] for r in eng_rows)
+    rows.append({"op": "llama3 layer (engine form: 4 launches)", "us": round(us, 3),
+                 "GBps": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4),
+                 "bytes": nbytes})
     return rows
 
 
