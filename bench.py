@@ -951,8 +951,27 @@ def gemm_profile_pass(T: int = 512, M: int = 11008, K: int = 4096, copies: int =
     stream = Stream()
     for i in range(launches):
         native.check(lib.asmhip_gemm_q8_0(wbufs[i % copies].ptr, dq.ptr, dc.ptr, T, M, K, stream.handle), "gemm")
+    # the same product on split operands (int8 qs planes + fp32 scale planes)
+    nb = K // 32
+    w0 = wbufs[0].download(np.uint8, (M, nb, 34))
+    a0 = dq.download(np.uint8, (T, nb, 34))
+    planes = [DeviceBuffer.from_numpy(v) for v in (
+        np.ascontiguousarray(w0[:, :, 2:]).view(np.int8), w0[:, :, 0:2].copy().view(np.float16).reshape(M, nb).astype(np.float32),
+        np.ascontiguousarray(a0[:, :, 2:]).view(np.int8), a0[:, :, 0:2].copy().view(np.float16).reshape(T, nb).astype(np.float32))]
+    for b in wbufs[1:]:
+        b.close()
+    wsplit = [(planes[0], planes[1])]
+    for _ in range(copies - 1):
+        q, sc = DeviceBuffer(planes[0].nbytes), DeviceBuffer(planes[1].nbytes)
+        q.copy_from(planes[0])
+        sc.copy_from(planes[1])
+        wsplit.append((q, sc))
+    for i in range(launches):
+        q, sc = wsplit[i % copies]
+        native.check(lib.asmhip_gemm_q8_split(q.ptr, sc.ptr, planes[2].ptr, planes[3].ptr, dc.ptr, T, M, K,
+                                              stream.handle), "gemm split")
     stream.synchronize()
-    log(f"GEMM profile pass: {launches} launches ({T}x{M}x{K})")
+    log(f"GEMM profile pass: {launches} launches of each layout ({T}x{M}x{K})")
 
 
 # rocprofv3 passes for the GEMM (each within one pass's limit of 8 SQ and 2 GRBM
@@ -969,13 +988,22 @@ def gemm_counters(T: int = 512, M: int = 11008, K: int = 4096, timeout_s: int = 
     """Hardware counters of the Q8_0 GEMM per dispatch and what they give:
     matrix-core busy fraction, int8 ops counted by the hardware (MOPS_I8 x 512)
     against 2 T M K, VALU instructions per 32x32 output tile and block, the shader
-    clock (GUI-active cycles per XCD over the dispatch's duration)."""
-    from asmllm_amd.device import device_info
-
-    res = _pmc_passes(GEMM_PASSES, ["--gemm-profile-pass"], {"gemm": lambda n: "gemm_q8_0" in n}, timeout_s)
+    clock (GUI-active cycles per XCD over the dispatch's duration); for the
+    block-form kernel and, under "split_layout", the split-operand one."""
+    res = _pmc_passes(GEMM_PASSES, ["--gemm-profile-pass"],
+                      {"gemm": lambda n: "gemm_q8_0" in n, "split": lambda n: "gemm_q8_split" in n}, timeout_s)
     if res is None:
         return None
-    v, us = res["gemm"]["counters"], res["gemm"]["us"]
+    out = _gemm_derived(res["gemm"], T, M, K)
+    if "split" in res:
+        out["split_layout"] = _gemm_derived(res["split"], T, M, K)
+    return out
+
+
+def _gemm_derived(r: dict, T: int, M: int, K: int) -> dict:
+    from asmllm_amd.device import device_info
+
+    v, us = r["counters"], r["us"]
     cus = device_info()["compute_units"]
     simds, xcds = 4 * cus, 8
     gui = v["GRBM_GUI_ACTIVE"] / xcds  # summed over the XCDs' GRBMs
@@ -984,7 +1012,7 @@ def gemm_counters(T: int = 512, M: int = 11008, K: int = 4096, timeout_s: int = 
     return {
         "workload": f"Q8_0 GEMM C[{T}][{M}] = A_q8[{T}][{K}] . W_q8[{M}][{K}]^T, eager launches",
         "dispatch_us": round(us, 3),
-        "dispatches": res["gemm"]["dispatches"],
+        "dispatches": r["dispatches"],
         "counters": {k: round(x, 1) for k, x in v.items()},
         "gui_cycles": round(gui, 0),
         "shader_clock_ghz": round(gui / us / 1e3, 3),
