@@ -393,9 +393,9 @@ __global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* _
 // [rows][K/32], the operand layout of the reference's asm_matmul_q8
 // (matmul_q8_avx2.asm:51-194: qweights int8[M][K/32][32], scales f32[M][K/32]).
 // A K step of two blocks is 64 contiguous qs bytes and 8 scale bytes per row.
-// qs rows are parked at an 80-byte pitch (five 16-byte units, an odd number:
-// each group of 8 lanes of a 32-row b128 operand read covers the 8 bank quads
-// once), so an operand is one aligned ds_read_b128 with no realignment.  The
+// qs rows are parked at an 80-byte pitch (five 16-byte units; the counters
+// still show bank conflicts on 35% of LDS-active cycles), so an operand is one
+// aligned ds_read_b128 with no realignment.  The
 // scale product d_a d_w comes from v_mfma_f32_32x32x2_f32 with the scales in
 // k = 0 and zeros in k = 1: one fp32 product per output, rounded once, as the
 // CPU's fmul, for any fp32 scales.  The k = 1 lanes read their zeros from a
