@@ -39,6 +39,11 @@ HIPCC_FLAGS = [
     "-O3",
     "-mllvm",
     "-amdgpu-mfma-vgpr-form",
+    # the first 16 dwords of every kernel's arguments arrive in SGPRs at wave
+    # launch instead of through a scalar load (gfx950 firmware preloads them;
+    # the compiler keeps a loading prologue for firmware that does not)
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     "-std=c++17",
     "-fPIC",
     "-fvisibility=hidden",
