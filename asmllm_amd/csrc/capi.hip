@@ -719,6 +719,20 @@ extern "C" int asmhip_stream_read(const void* buf, int64_t bytes, void* sink, vo
     return stream_read_launch(buf, bytes, static_cast<uint32_t*>(sink), (hipStream_t)stream);
 }
 
+extern "C" int asmhip_stream_read_shaped(const void* buf, int64_t bytes, const float* x, int xn, float* y,
+                                         int64_t y_floats, int flags, int lds, void* sink, void* stream) {
+    return shaped_read_launch(buf, bytes, x, xn, y, y_floats, flags, lds, static_cast<uint32_t*>(sink),
+                              (hipStream_t)stream);
+}
+
+extern "C" int asmhip_empty_launch(int grid, int threads, int lds, void* stream) {
+    return empty_launch(grid, threads, lds, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_grid_barrier(unsigned* counter, int n, unsigned* err, void* stream) {
+    return grid_barrier_launch(counter, n, err, (hipStream_t)stream);
+}
+
 extern "C" int64_t asmhip_attention_decode_noalloc_max_floats(void) { return kNoAllocScratchFloats; }
 
 extern "C" int asmhip_attention_decode_rope_noalloc(const float* qkv, void* k_cache, void* v_cache, float* out,

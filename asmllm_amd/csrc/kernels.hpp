@@ -89,6 +89,16 @@ int gemm_q8_split_launch(const int8_t* wq, const float* wsc, const int8_t* aq, c
 // Plain streaming read of `bytes` in one launch (measurement: the single-launch
 // read floor); `sink` is 4 KB of device memory the kernel practically never writes.
 int stream_read_launch(const void* buf, int64_t bytes, uint32_t* sink, hipStream_t st);
+// The same read in the matvec's launch shape (one 1024-thread workgroup per
+// compute unit), flags: 1 the matvec's dynamic LDS (`lds` bytes), 2 x (`xn`
+// floats) read and a workgroup barrier first, 4 16 floats of y stored per workgroup.
+int shaped_read_launch(const void* buf, int64_t bytes, const float* x, int xn, float* y, int64_t y_floats, int flags,
+                       int lds, uint32_t* sink, hipStream_t st);
+// An empty kernel of the given shape (the cost of a launch that does nothing).
+int empty_launch(int grid, int threads, int lds, hipStream_t st);
+// n grid-wide barriers in one cooperative launch of one 1024-thread workgroup per
+// compute unit; *err is set if a barrier does not complete within its poll bound.
+int grid_barrier_launch(unsigned* counter, int n, unsigned* err, hipStream_t st);
 
 // Exact fp32 dequantization of GGUF blocks, row-major [rows][K].
 int dequant_launch(QuantType qt, const void* w, float* out, int64_t rows, int64_t K, hipStream_t stream);

@@ -80,6 +80,9 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_attention_decode_partials_rope_table": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, _P, _P]),
     "asmhip_matmul_attn_output": (c_int, [c_int, _P, _P, _P, _P, c_int64, c_int, c_int, c_int, c_int, _P]),
     "asmhip_stream_read": (c_int, [_P, c_int64, _P, _P]),
+    "asmhip_stream_read_shaped": (c_int, [_P, c_int64, _P, c_int, _P, c_int64, c_int, c_int, _P, _P]),
+    "asmhip_empty_launch": (c_int, [c_int, c_int, c_int, _P]),
+    "asmhip_grid_barrier": (c_int, [_P, c_int, _P, _P]),
     "asmhip_attention_decode_noalloc_max_floats": (c_int64, []),
     "asmhip_attention_decode_rope_noalloc": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, c_float, _P]),
     "asmhip_embed_q4_0": (c_int, [_P, _P, _P, c_int, c_int, _P]),

@@ -581,13 +581,99 @@ def bench_read_floor(multiples=(1, 2, 4, 8)) -> dict:
 
     launch_us = time_launches(enqueue_tiny, 64, reps=50)
     log(f"stream read 4 KB (launch floor): {launch_us:.3f} us")
+
+    # an empty kernel as a dependent graph node, at the matvec's launch shape
+    # (256 workgroups of 1024 threads, 155 KB of dynamic LDS) and two small ones
+    empty = []
+    for grid, threads, lds in ((256, 1024, 155 * 1024), (256, 256, 0), (64, 64, 0)):
+        def enqueue_empty(i, st, grid=grid, threads=threads, lds=lds):
+            native.check(lib.asmhip_empty_launch(grid, threads, lds, st), "empty launch")
+
+        us = time_launches(enqueue_empty, 64, reps=50)
+        empty.append({"grid": grid, "threads": threads, "lds_bytes": lds, "us": round(us, 3)})
+        log(f"empty launch {grid}x{threads}, {lds} B LDS: {us:.3f} us")
+
+    # the read floor in the matvec's launch shape, its structural pieces added one at a time
+    cus = device_info_cus()
+    x = DeviceBuffer(4 * K_MAIN)
+    native.check(lib.asmhip_fill_f32(x.ptr, K_MAIN, 0.5, None), "fill")
+    y_floats = 1 << 16
+    y = DeviceBuffer(4 * y_floats)
+    shaped = []
+    launches = region // unit
+    for flags, what in ((0, "one 1024-thread workgroup per CU, all loads up front"),
+                        (1, "+ the matvec's 155 KB of dynamic LDS"),
+                        (3, "+ x (16 KB) read and a workgroup barrier first"),
+                        (7, "+ 16 floats stored per workgroup at the end")):
+        def enqueue_shaped(i, st, flags=flags):
+            native.check(lib.asmhip_stream_read_shaped(buf.ptr + i * unit, unit, x.ptr, K_MAIN, y.ptr, y_floats,
+                                                       flags, 155 * 1024, sink.ptr, st), "shaped read")
+
+        us = time_launches(enqueue_shaped, launches, reps=max(4, 2000 // launches))
+        shaped.append({"flags": flags, "shape": what, "us": round(us, 3), "GBps": round(unit / us / 1e3, 1)})
+        log(f"shaped read ({what}): {us:.3f} us")
+    x.close()
+    y.close()
     buf.close()
     sink.close()
     return {"points": points, "fixed_us_per_launch": round(float(fixed), 3),
             "sustained_GBps": round(1e-3 / float(slope), 1),
             "floor_us_at_matvec_bytes": points[0]["us"],
             "floor_frac_of_peak": round(points[0]["GBps"] / HBM_PEAK_GBPS, 4),
-            "launch_floor_us_4KB": round(launch_us, 3)}
+            "launch_floor_us_4KB": round(launch_us, 3),
+            "empty_launch": empty,
+            "matvec_shaped_read": shaped,
+            "grid_barrier": bench_grid_barrier(cus)}
+
+
+def device_info_cus() -> int:
+    from asmllm_amd.device import device_info
+
+    return int(device_info()["compute_units"])
+
+
+def bench_grid_barrier(cus: int) -> dict | None:
+    """What a grid-wide handoff inside one launch costs: n barriers in one
+    cooperative launch of one 1024-thread workgroup per compute unit (a counter
+    added to and polled at agent scope, coherent across the XCDs), timed at
+    n = 200 and 1000; the difference over 800 is the cost of one barrier, to set
+    beside a dependent launch (`empty_launch`)."""
+    from asmllm_amd import native
+    from asmllm_amd.device import DeviceBuffer, Event, Stream
+
+    lib = native.lib()
+    counter, err = DeviceBuffer(256), DeviceBuffer(256)
+    zero = np.zeros(64, np.uint32)
+    counter.upload(zero)
+    err.upload(zero)
+    stream = Stream()
+    e0, e1 = Event(timing=True), Event(timing=True)
+
+    def run(n: int) -> float | None:
+        e0.record(stream)
+        rc = lib.asmhip_grid_barrier(counter.ptr, n, err.ptr, stream.handle)
+        if rc:
+            log(f"grid barrier not measured: {native.last_error()}")
+            return None
+        e1.record(stream)
+        e1.synchronize()
+        if int(err.download(np.uint32, 1)[0]):
+            log("grid barrier: a barrier hit its poll bound")
+            return None
+        return e0.elapsed_ms(e1) * 1e3
+
+    times = {}
+    for n in (0, 200, 1000, 200, 1000):
+        t = run(n)
+        if t is None:
+            return None
+        times.setdefault(n, []).append(t)
+    per = (min(times[1000]) - min(times[200])) / 800
+    log(f"grid barrier: {per:.3f} us per barrier ({cus} workgroups)")
+    counter.close()
+    err.close()
+    return {"workgroups": cus, "us_per_barrier": round(per, 3), "launch_us_n0": round(min(times[0]), 2),
+            "us_n200": round(min(times[200]), 1), "us_n1000": round(min(times[1000]), 1)}
 
 
 def bench_matvec_phases(K: int = K_MAIN, rows=(1024, 2048, 4096, 8192, 11008, 16384, 22016, 32000),
@@ -898,6 +984,67 @@ def _pmc_passes(passes, workload: list[str], kinds: dict, timeout_s: int = 150) 
     return {k: {"counters": vals[k], "us": float(np.mean(durs[k])), "dispatches": len(durs[k])} for k in kinds}
 
 
+HEADLINE_KERNEL = "gguf_mfma_stream<0, 1, 16, 1, 1, 0, false, 16>"
+
+
+def kernel_trace(steps: int = 20, timeout_s: int = 300) -> dict | None:
+    """rocprofv3 kernel trace of bench.py's own timed region: the default matvec
+    run (`steps` launches queued behind the untimed cover reads, no other legs) in
+    a child process under `rocprofv3 --kernel-trace`.  The last `steps` dispatches
+    of the headline kernel are the timed launches; their begin/end timestamps give
+    each launch's duration in the same back-to-back regime as bench.py's events
+    (the tracer's own host work per launch runs while the cover keeps the GPU
+    busy, so the timed launches still start back to back).  Returns their mean
+    duration next to the child's own HIP-event figure, or None without rocprofv3."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        log("rocprofv3 not found: kernel trace not taken")
+        return None
+    env = dict(os.environ, TMPDIR="/tmp")
+    workload = ["--steps", str(steps), "--warmup", "5", "--no-extra", "--no-cpu", "--no-traffic", "--no-trace"]
+    with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+        cmd = [exe, "--kernel-trace", "--output-format", "csv", "-d", tmp, "-o", "trace", "--",
+               sys.executable, str(ROOT / "bench.py"), *workload]
+        try:
+            out = subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout_s, check=True, capture_output=True,
+                                 text=True).stdout
+        except (subprocess.SubprocessError, OSError) as e:
+            log(f"rocprofv3 kernel trace failed ({e})")
+            return None
+        files = list(Path(tmp).rglob("trace_kernel_trace.csv"))
+        if not files:
+            log("rocprofv3 wrote no kernel trace")
+            return None
+        with open(files[0]) as f:
+            rows = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in csv.DictReader(f)
+                    if HEADLINE_KERNEL in r["Kernel_Name"]]
+    rows.sort()
+    if len(rows) < steps:
+        log(f"kernel trace holds {len(rows)} headline dispatches, fewer than {steps}")
+        return None
+    try:
+        child = json.loads(out.strip().splitlines()[-1])
+    except (ValueError, IndexError):
+        child = {}
+    timed = rows[-steps:]
+    dur = np.array([(e - b) / 1e3 for b, e in timed])
+    gaps = np.array([(timed[i + 1][0] - timed[i][1]) / 1e3 for i in range(steps - 1)])
+    bytes_step = q4_algorithmic_bytes(M_MAIN, K_MAIN)
+    mean = float(dur.mean())
+    return {"command": "rocprofv3 --kernel-trace -- python3 bench.py " + " ".join(workload),
+            "kernel": HEADLINE_KERNEL, "dispatches_traced": len(rows), "timed_dispatches": steps,
+            "us_mean": round(mean, 3), "us_median": round(float(np.median(dur)), 3),
+            "us_min": round(float(dur.min()), 3), "us_max": round(float(dur.max()), 3),
+            "gap_us_mean": round(float(gaps.mean()), 3), "gap_us_max": round(float(gaps.max()), 3),
+            "frac_at_trace_mean": round(bytes_step / mean / 1e3 / HBM_PEAK_GBPS, 4),
+            "child_events_us_per_step": round(child["ms_per_step"] * 1e3, 3) if "ms_per_step" in child else None}
+
+
 def measure_traffic(timeout_s: int = 150) -> dict | None:
     """HBM bytes per matvec launch from the L2's memory requests counted by size:
     read = 32 RDREQ_32B + 64 RDREQ_64B + 128 RDREQ_128B, written = 64 WRREQ_64B +
@@ -1043,9 +1190,10 @@ def main() -> None:
     ap.add_argument("--gemm-profile-pass", action="store_true",
                     help="run only a short fixed GEMM workload for hardware-counter collection")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--no-trace", action="store_true", help="skip the rocprofv3 kernel trace of the timed region")
     ap.add_argument("--no-extra", action="store_true", help="skip the shape table, GEMM and decode legs")
     ap.add_argument("--only", choices=["decode", "gemm", "table", "floor", "host", "cpu", "traffic", "gemm_counters",
-                                       "phases"],
+                                       "phases", "trace"],
                     help="run one extra leg and print its JSON")
     ap.add_argument("--eager", action="store_true", help="with --only: launch without graphs")
     args = ap.parse_args()
@@ -1073,7 +1221,8 @@ def main() -> None:
         else:
             res = {"gemm": bench_gemm, "table": bench_matvec_table, "floor": bench_read_floor,
                    "host": bench_host_pointer, "traffic": measure_traffic,
-                   "gemm_counters": gemm_counters, "phases": bench_matvec_phases}[args.only]()
+                   "gemm_counters": gemm_counters, "phases": bench_matvec_phases,
+                   "trace": kernel_trace}[args.only]()
         print(json.dumps({args.only: res}), flush=True)
         return
 
@@ -1090,6 +1239,7 @@ def main() -> None:
         extra["host_pointer"] = bench_host_pointer()
     cpu = None if args.no_cpu else bench_cpu_baseline(args.cpu_seconds)
     traffic = None if args.no_traffic else measure_traffic()
+    trace = None if args.no_trace else kernel_trace()
 
     result = {
         "metric": METRIC,
@@ -1123,6 +1273,7 @@ def main() -> None:
             "kernel_us_mean": round(mv["kernel_us_mean"], 3),
             "fp32_valu_kernel_us_mean": round(mv["fp32_kernel_us_mean"], 3),
             "bytes_per_launch": mv["bytes_per_step"],
+            "kernel_trace": trace,
         },
         "cpu_baseline": cpu,
         "parity_max_err_over_l1": mv["parity_max_err_over_l1"],

@@ -279,6 +279,24 @@ ASMHIP_API int asmhip_matmul_attn_output(int qtype, const void* blocks, const fl
  * single-launch read floor a matvec over the same bytes can approach (no
  * counterpart in the reference). */
 ASMHIP_API int asmhip_stream_read(const void* buf, int64_t bytes, void* sink, void* stream);
+/* Measurement, not part of the path (no counterpart in the reference): the same
+ * read in the launch shape of the matvec (one 1024-thread workgroup per compute
+ * unit, all loads up front) with the matvec's structural pieces added by `flags`:
+ * 1 = its dynamic LDS allocation of `lds` bytes (<= 160 KB), 2 = x (`xn` floats,
+ * 16-byte aligned) read and a workgroup barrier before the loads, 4 = 16 floats of
+ * `y` (`y_floats` floats, at least 16 per workgroup) stored per workgroup at the
+ * end.  `sink` is 4 KB of device memory. */
+ASMHIP_API int asmhip_stream_read_shaped(const void* buf, int64_t bytes, const float* x, int xn, float* y,
+                                         int64_t y_floats, int flags, int lds, void* sink, void* stream);
+/* Measurement (no counterpart in the reference): an empty kernel of `grid`
+ * workgroups of `threads` threads with `lds` bytes of dynamic LDS. */
+ASMHIP_API int asmhip_empty_launch(int grid, int threads, int lds, void* stream);
+/* Measurement (no counterpart in the reference): `n` grid-wide barriers inside
+ * one cooperative launch of one 1024-thread workgroup per compute unit, over a
+ * zero-initialized device counter; *err (device) becomes nonzero if a barrier
+ * does not complete within its bounded poll.  ASMHIP_ERR_UNSUPPORTED without
+ * cooperative launch. */
+ASMHIP_API int asmhip_grid_barrier(unsigned* counter, int n, unsigned* err, void* stream);
 /* asmhip_attention_decode_rope without the workspace argument.  No counterpart
  * in the reference: it is for callers that cannot allocate device memory (HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
