@@ -699,12 +699,20 @@ constexpr int64_t kNoAllocScratchFloats = 1 << 20;  // 4 MiB: n_heads * splits *
 __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 float* g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_for_current_device(float** out) {
+int scratch_for_current_device(float** out, hipStream_t st) {
     int dev = 0;
     const int rc = current_device(&dev);
     if (rc) return rc;
     std::lock_guard<std::mutex> lock(g_mu);
     if (!g_scratch_ptr[dev]) {
+        // the address is looked up on the first call on each device; that lookup is
+        // not a stream operation, so it is kept out of stream capture
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        ASMHIP_TRY(hipStreamIsCapturing(st, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(kInvalidArgument,
+                        "attention without a workspace: the first call on a device must be made outside stream "
+                        "capture (it looks up the device's scratch address); make one call before capturing");
         void* p = nullptr;
         ASMHIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         if (!p) return fail(kHipError, "hipGetSymbolAddress returned no address for the attention scratch");
@@ -749,7 +757,7 @@ extern "C" int asmhip_attention_decode_rope_noalloc(const float* qkv, void* k_ca
                     n_heads, attn_decode_splits(max_ctx), head_dim, (long long)need,
                     (long long)kNoAllocScratchFloats);
     float* part = nullptr;
-    const int rc = scratch_for_current_device(&part);
+    const int rc = scratch_for_current_device(&part, (hipStream_t)stream);
     if (rc) return rc;
     return attn_decode_launch(qkv, k_cache, v_cache, part, out, n_heads, n_kv_heads, head_dim, pos_dev, max_ctx,
                               true, theta, (hipStream_t)stream);
@@ -772,6 +780,12 @@ extern "C" int asmhip_embed_q8_0(const void* table, const int* token_dev, float*
 extern "C" int asmhip_argmax(const float* logits, int n, int* token_dev, int* pos_dev, void* stream) {
     if (!logits || !token_dev) return fail(kInvalidArgument, "null pointer argument");
     return argmax_launch(logits, n, token_dev, pos_dev, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_argmax_history(const float* logits, int n, int* token_dev, int* pos_dev, int* history_dev,
+                                     int history_len, void* stream) {
+    if (!logits || !token_dev || !pos_dev || !history_dev) return fail(kInvalidArgument, "null pointer argument");
+    return argmax_launch(logits, n, token_dev, pos_dev, (hipStream_t)stream, history_dev, history_len);
 }
 
 // ---- plumbing --------------------------------------------------------------------

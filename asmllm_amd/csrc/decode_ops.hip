@@ -512,7 +512,8 @@ __device__ __forceinline__ bool argmax_better(float a, int ia, float b, int ib) 
 // change the result (ties go to the lower index).
 template <bool VEC>
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                      int* __restrict__ token, int* __restrict__ pos) {
+                                                      int* __restrict__ token, int* __restrict__ pos,
+                                                      int* __restrict__ history, int history_len) {
     __shared__ float bv[16];
     __shared__ int bi[16];
     float v = -INFINITY;
@@ -579,7 +580,13 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
                 bidx = bi[i];
             }
         *token = bidx;
-        if (pos) *pos = *pos + 1;
+        if (pos) {
+            // history[p] = the token chosen at position p, so that a graph of
+            // several steps keeps every token, not just the last one
+            const int p = *pos;
+            if (history && p >= 0 && p < history_len) history[p] = bidx;
+            *pos = p + 1;
+        }
     }
 }
 
@@ -768,12 +775,16 @@ int embed_launch(QuantType qt, const void* table, const int* token, float* x, in
     return kOk;
 }
 
-int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st) {
+int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st, int* history, int history_len) {
     if (n <= 0) return fail(kInvalidArgument, "argmax: empty input");
+    if (history && (!pos || history_len <= 0))
+        return fail(kInvalidArgument, "argmax: a token history needs the position and a length");
     if (n % 4 == 0 && (uintptr_t)logits % 16 == 0)
-        hipLaunchKernelGGL(argmax_kernel<true>, dim3(1), dim3(1024), 0, st, logits, n, token, pos);
+        hipLaunchKernelGGL(argmax_kernel<true>, dim3(1), dim3(1024), 0, st, logits, n, token, pos, history,
+                           history_len);
     else
-        hipLaunchKernelGGL(argmax_kernel<false>, dim3(1), dim3(1024), 0, st, logits, n, token, pos);
+        hipLaunchKernelGGL(argmax_kernel<false>, dim3(1), dim3(1024), 0, st, logits, n, token, pos, history,
+                           history_len);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

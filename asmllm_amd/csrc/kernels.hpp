@@ -168,6 +168,9 @@ int rope_table_launch(float* table, int hd, int max_ctx, float theta, hipStream_
 
 // x = row *token of a Q4_0 or Q8_0 GGUF table [n_vocab][dim], exact.
 int embed_launch(QuantType qt, const void* table, const int* token, float* x, int n_vocab, int dim, hipStream_t st);
-int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st);
+// *token = argmax; with pos: history[*pos] = *token (when history and 0 <= *pos <
+// history_len), then ++*pos.
+int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st, int* history = nullptr,
+                  int history_len = 0);
 
 }  // namespace asmhip

@@ -17,8 +17,10 @@ stream, so it can be captured once into a HIP graph and replayed per token:
     matvecs (accumulate);
   * the token id and the position live in device ints: the embedding kernel
     reads the token, RoPE / the KV write / attention read the position, and
-    the argmax kernel writes the next token and advances the position, so a
-    replayed graph walks the sequence without host involvement;
+    the argmax kernel writes the next token, records it in a device history
+    indexed by position and advances the position, so a replayed graph of one
+    or many token steps walks the sequence without host involvement and keeps
+    every token it chose;
   * RoPE and the KV-cache write are fused into the attention launch
     (asmhip_attention_decode_partials_rope_table), its cos/sin read from a
     table of every position's angles formed once at set-up
@@ -196,8 +198,11 @@ class DecodeEngine:
                                          self.stream.handle), "rope table")
         self.token = DeviceBuffer(4)
         self.pos = DeviceBuffer(4)
+        # history[p] = the greedy token chosen at position p (written by the argmax launch)
+        self.history = DeviceBuffer(4 * self.max_ctx)
         self.vocab: list[str] = []
         self._graph: Graph | None = None
+        self._multi: dict[int, Graph] = {}
 
     # ---- model data ---------------------------------------------------------------
 
@@ -352,7 +357,8 @@ class DecodeEngine:
                   "gate/up matvec + swiglu")
             mv(ly.wdown, self.ffn.ptr, self.x.ptr, d, h, NONE, None, 1, "down matvec")
         normed(self.final_norm, s.vocab, self.output, self.logits.ptr, "lm-head matvec", self.output_type)
-        check(L.asmhip_argmax(self.logits.ptr, s.vocab, self.token.ptr, self.pos.ptr, st), "argmax")
+        check(L.asmhip_argmax_history(self.logits.ptr, s.vocab, self.token.ptr, self.pos.ptr, self.history.ptr,
+                                      self.max_ctx, st), "argmax")
 
     def set_position(self, token_id: int, pos: int) -> None:
         if not 0 <= pos < self.max_ctx:
@@ -378,30 +384,52 @@ class DecodeEngine:
 
     def capture_steps(self, n_steps: int) -> Graph:
         """n_steps consecutive token steps as one HIP graph (the caller closes it).
-        Each step reads the token and position the previous one left on the GPU,
-        so one replay decodes n_steps tokens with one graph launch instead of
-        n_steps (a graph launch costs ~7 us before its first kernel starts); the
-        intermediate tokens are not kept, the last one is in `token`."""
+        Each step reads the token and position the previous one left on the GPU
+        and records its token in `history`, so one replay decodes n_steps tokens
+        with one graph launch instead of n_steps (a graph launch costs ~7 us
+        before its first kernel starts)."""
         if n_steps < 1:
             raise ValueError("n_steps must be >= 1")
         return Graph.capture(self.stream, lambda: [self.enqueue_step() for _ in range(n_steps)])
 
+    STEPS_PER_GRAPH = 16
+
+    def enqueue_generate(self, n_steps: int, use_graph: bool = True) -> None:
+        """Enqueues n_steps token steps from the token and position on the GPU
+        (no synchronization): replays of a cached graph of STEPS_PER_GRAPH steps,
+        then one-step replays for the rest; or direct launches."""
+        if not use_graph:
+            for _ in range(n_steps):
+                self.enqueue_step()
+            return
+        per = self.STEPS_PER_GRAPH
+        if n_steps >= per and per not in self._multi:
+            self._multi[per] = self.capture_steps(per)
+        for _ in range(n_steps // per):
+            self._multi[per].launch(self.stream)
+        rest = n_steps % per
+        if rest:
+            one = self.capture()
+            for _ in range(rest):
+                one.launch(self.stream)
+
+    def read_history(self, pos: int, n: int) -> list[int]:
+        """The greedy tokens chosen at positions pos .. pos + n - 1."""
+        if pos < 0 or pos + n > self.max_ctx:
+            raise ValueError("history range outside the cache")
+        return [int(t) for t in self.history.download(np.int32, (n,), offset=4 * pos)]
+
     def generate(self, token_id: int, pos: int, n_steps: int, use_graph: bool = True) -> list[int]:
         """Greedy decode of n_steps tokens starting from token_id at pos
-        (the loop of generate.py:411-430, argmax on the GPU)."""
+        (the loop of generate.py:411-430, argmax on the GPU).  Every step is
+        enqueued before the host waits: the tokens come back from the device
+        history in one copy at the end."""
         if pos + n_steps > self.max_ctx:
             raise ValueError("decode would run past the KV cache")
         self.set_position(token_id, pos)
-        out = []
-        graph = self.capture() if use_graph else None
-        for _ in range(n_steps):
-            if graph is not None:
-                graph.launch(self.stream)
-            else:
-                self.enqueue_step()
-            self.stream.synchronize()
-            out.append(int(self.token.download(np.int32, (1,))[0]))
-        return out
+        self.enqueue_generate(n_steps, use_graph)
+        self.stream.synchronize()
+        return self.read_history(pos, n_steps)
 
     def read_position(self) -> int:
         return int(self.pos.download(np.int32, (1,))[0])
@@ -410,3 +438,6 @@ class DecodeEngine:
         if self._graph is not None:
             self._graph.close()
             self._graph = None
+        for g in self._multi.values():
+            g.close()
+        self._multi.clear()

@@ -88,6 +88,7 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_embed_q4_0": (c_int, [_P, _P, _P, c_int, c_int, _P]),
     "asmhip_embed_q8_0": (c_int, [_P, _P, _P, c_int, c_int, _P]),
     "asmhip_argmax": (c_int, [_P, c_int, _P, _P, _P]),
+    "asmhip_argmax_history": (c_int, [_P, c_int, _P, _P, _P, c_int, _P]),
     # plumbing
     "asmhip_device_count": (c_int, []),
     "asmhip_device_info": (c_int, [c_char_p, c_size_t, POINTER(c_int), POINTER(c_int), POINTER(c_size_t)]),

@@ -827,51 +827,40 @@ def decode_cpu_baseline(eng, context: int, seconds: float) -> dict:
 def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: bool = False,
                  cpu_seconds: float = 0.0) -> dict:
     """Greedy single-token decode of the 32-layer 7B-shape Q4_0 model, fp16 KV
-    cache prefilled to `context`: `steps` tokens from position `context`, as
-    replays of a captured graph of 16 consecutive token steps (token and
-    position stay on the GPU between steps; one graph launch per 16 tokens,
-    since a graph launch costs ~7 us before its first kernel) plus single-step
-    replays for the remainder.  `eager` enqueues the launches directly instead
-    (for tracing tools that do not follow graph launches)."""
+    cache prefilled to `context`: `steps` tokens from position `context` through
+    the engine's own generation path (DecodeEngine.enqueue_generate): replays of
+    a captured graph of 16 consecutive token steps (token, position and the
+    history of chosen tokens stay on the GPU between steps; one graph launch per
+    16 tokens, since a graph launch costs ~7 us before its first kernel) plus
+    single-step replays for the remainder; every generated token is read back
+    from the device history after the timed region.  `eager` enqueues the
+    launches directly instead (for tracing tools that do not follow graph
+    launches)."""
     from asmllm_amd.device import Event, synchronize
     from asmllm_amd.engine import LLAMA_7B, DecodeEngine
 
     s = LLAMA_7B
     eng = DecodeEngine(s, max_ctx=context + steps)
     eng.init_random(seed=42)
-    per_graph = 16
-    multi = None
-    if eager:
-        step = eng.enqueue_step
-    else:
-        graph = eng.capture()
-        multi = eng.capture_steps(per_graph) if steps >= per_graph else None
-
-        def step():
-            graph.launch(eng.stream)
-
+    per_graph = eng.STEPS_PER_GRAPH
+    # warm-up: every graph the timed steps replay is launched once (a graph's
+    # first launch also sets it up on the device)
     eng.set_position(1, context)
-    for _ in range(warmup):
-        step()
-    if multi is not None:  # a graph's first launch also sets it up on the device
-        multi.launch(eng.stream)
+    eng.enqueue_generate(max(warmup, per_graph + 1) if not eager else warmup, use_graph=not eager)
     eng.stream.synchronize()
     eng.set_position(1, context)
     synchronize()
     e0, e1 = Event(timing=True), Event(timing=True)
     e0.record(eng.stream)
-    done = 0
-    if multi is not None:
-        for _ in range(steps // per_graph):
-            multi.launch(eng.stream)
-        done = steps // per_graph * per_graph
-    for _ in range(steps - done):
-        step()
+    # the engine's own generation path: graphs of 16 token steps, then one-step
+    # graphs for the rest; every token is kept in the device history
+    eng.enqueue_generate(steps, use_graph=not eager)
     e1.record(eng.stream)
     e1.synchronize()
     ms = e0.elapsed_ms(e1)
-    if multi is not None:
-        multi.close()
+    tokens = eng.read_history(context, steps)
+    if len(tokens) != steps or not all(0 <= t < s.vocab for t in tokens):
+        raise SystemExit("decode: the token history is not a list of vocabulary ids")
     end_pos = eng.read_position()
     if end_pos != context + steps:
         raise SystemExit(f"decode: position {end_pos} after {steps} steps from {context}")

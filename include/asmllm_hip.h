@@ -177,12 +177,16 @@ ASMHIP_API int asmhip_matmul_swiglu(int qtype, const void* blocks, const float* 
  * applied to a batch; the reference itself has no GEMM. */
 ASMHIP_API int asmhip_gemm_q8_0(const void* w_blocks, const void* a_blocks, float* c, int64_t T, int64_t M,
                                 int64_t K, void* stream);
-/* The same GEMM on the split layout of asm_matmul_q8 (matmul_q8_avx2.asm:51-194): int8 qs
- * planes [rows][K] (16-byte aligned) and fp32 scale planes [rows][K/32], for W (M rows) and A
- * (T rows; quantize activations with asmhip_quantize_q8_split).  Per block the scale is the
- * fp32 product d_w * d_a (any fp32 scales), then acc = fmaf(float(dot), scale, acc) in block
- * order: with scales widened from fp16 the result is bitwise that of asmhip_gemm_q8_0 on the
- * same blocks. */
+/* The same GEMM with W in the split layout of asm_matmul_q8 (matmul_q8_avx2.asm:51-194):
+ * int8 qs planes [rows][K] (16-byte aligned) and fp32 scale planes [rows][K/32], for W (M rows)
+ * and A (T rows).  The activations are int8 too: quantize the fp32 rows with
+ * asmhip_quantize_q8_split (Q8_0, round to nearest even, scale amax/127 rounded to fp16).  So
+ * C is NOT T calls of asm_matmul_q8, which multiplies the int8 weights by fp32 x: each
+ * activation carries its quantization error, at most half its block's step d_a = amax/127
+ * (|C - asm_matmul_q8(W, x)| <= sum over the row of |w| d_a / 2, about 0.4% of the row's L1
+ * norm; tests/test_gemm_gpu.py measures it).  Per block the scale is the fp32 product
+ * d_w * d_a (any fp32 scales), then acc = fmaf(float(dot), scale, acc) in block order: with
+ * scales widened from fp16 the result is bitwise that of asmhip_gemm_q8_0 on the same blocks. */
 ASMHIP_API int asmhip_gemm_q8_split(const int8_t* w_qs, const float* w_scales, const int8_t* a_qs,
                                     const float* a_scales, float* c, int64_t T, int64_t M, int64_t K, void* stream);
 /* Process-wide Q4_0 GGUF kernel choice (ASMHIP_Q4_KERNEL_*). */
@@ -306,7 +310,9 @@ ASMHIP_API int asmhip_grid_barrier(unsigned* counter, int n, unsigned* err, void
  * max_ctx <= 3072, else ceil(max_ctx / 512)) are rejected with
  * ASMHIP_ERR_INVALID_ARGUMENT.  Calls that overlap on one GPU share the array and
  * race; nothing in it needs clearing between calls.  Same results, bit for bit,
- * as asmhip_attention_decode_rope. */
+ * as asmhip_attention_decode_rope.  The first call on each device looks up the
+ * array's address and must be made outside stream capture (inside a capture it
+ * returns ASMHIP_ERR_INVALID_ARGUMENT); later calls may be captured. */
 ASMHIP_API int64_t asmhip_attention_decode_noalloc_max_floats(void);
 ASMHIP_API int asmhip_attention_decode_rope_noalloc(const float* qkv, void* k_cache, void* v_cache, float* out,
                                                     int n_heads, int n_kv_heads, int head_dim, const int* pos_dev,
@@ -321,6 +327,13 @@ ASMHIP_API int asmhip_embed_q8_0(const void* table, const int* token_dev, float*
 /* *token_dev = first index of max(logits) (numpy.argmax, generate.py:419-420);
  * then ++*pos_dev when pos_dev is not NULL. */
 ASMHIP_API int asmhip_argmax(const float* logits, int n, int* token_dev, int* pos_dev, void* stream);
+/* asmhip_argmax that also records the token: history_dev[*pos_dev] = *token_dev
+ * (when 0 <= *pos_dev < history_len), then ++*pos_dev.  The generation loop of
+ * generate.py:411-430 appends each greedy token on the host; here the list is
+ * kept on the GPU, so a graph of several token steps returns every token, not
+ * only the last. */
+ASMHIP_API int asmhip_argmax_history(const float* logits, int n, int* token_dev, int* pos_dev, int* history_dev,
+                                     int history_len, void* stream);
 
 /* ---- device memory, streams, events (so a ctypes host needs no other GPU
  *      binding; the reference's buffers are numpy arrays) ----------------- */

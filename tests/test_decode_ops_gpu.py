@@ -249,6 +249,35 @@ def test_embed_row_and_argmax(hip, oracle):
     assert int(dpos.download(np.int32, 1)[0]) == 42
 
 
+def test_argmax_history_records_each_position(hip):
+    """asmhip_argmax_history: history[pos] = the token, then pos + 1; a position
+    outside [0, history_len) advances without writing."""
+    rng = np.random.default_rng(3)
+    n, hl = 32000, 8
+    dl, dtok, dpos = DeviceBuffer(4 * n), DeviceBuffer(4), DeviceBuffer(4)
+    dhist = DeviceBuffer(4 * hl)
+    dhist.upload(np.full(hl, -1, np.int32))
+    want = []
+    for p in (0, 3, 7):
+        logits = rng.standard_normal(n).astype(np.float32)
+        dl.upload(logits)
+        dpos.upload(np.array([p], np.int32))
+        _ok(hip, hip.asmhip_argmax_history(dl.ptr, n, dtok.ptr, dpos.ptr, dhist.ptr, hl, None))
+        synchronize()
+        assert int(dpos.download(np.int32, 1)[0]) == p + 1
+        want.append((p, int(np.argmax(logits))))
+    hist = dhist.download(np.int32, hl)
+    for p, t in want:
+        assert hist[p] == t
+    assert all(hist[p] == -1 for p in range(hl) if p not in (0, 3, 7))
+    dpos.upload(np.array([hl], np.int32))  # past the history: no write
+    _ok(hip, hip.asmhip_argmax_history(dl.ptr, n, dtok.ptr, dpos.ptr, dhist.ptr, hl, None))
+    synchronize()
+    assert int(dpos.download(np.int32, 1)[0]) == hl + 1
+    np.testing.assert_array_equal(dhist.download(np.int32, hl), hist)
+    assert hip.asmhip_argmax_history(dl.ptr, n, dtok.ptr, None, dhist.ptr, hl, None) != 0
+
+
 @pytest.mark.parametrize("n", [1, 5, 36, 1024, 32000, 32768, 32769, 128256])
 def test_argmax_sizes_and_ties(hip, n):
     """One pass (n <= 32768) and several (the Llama-3 vocabulary), with 16-byte

@@ -149,8 +149,34 @@ def test_multi_step_graph_matches_single_step_replays():
     eng.stream.synchronize()
     assert eng.read_position() == 25
     assert int(eng.token.download(np.int32, (1,))[0]) == single[-1]
+    # every step of the graph recorded its token, not only the last one
+    assert eng.read_history(20, 5) == single
     np.testing.assert_array_equal(eng.logits.download(np.float32, shape.vocab), logits_single)
     multi.close()
+    eng.close()
+
+
+def test_generate_through_multi_step_graphs_keeps_every_token():
+    """generate() with more steps than one graph holds (16 + 16 + 3: two replays
+    of the 16-step graph, then one-step replays) returns the same tokens, bit for
+    bit the same final logits, as launching every step directly and reading the
+    token after each one."""
+    shape = SMALL[0]
+    eng = DecodeEngine(shape, max_ctx=96)
+    eng.init_random(seed=9)
+    n, pos0 = 35, 30
+    step_by_step = []
+    eng.set_position(4, pos0)
+    for _ in range(n):
+        eng.enqueue_step()
+        eng.stream.synchronize()
+        step_by_step.append(int(eng.token.download(np.int32, (1,))[0]))
+    logits_eager = eng.logits.download(np.float32, shape.vocab)
+    graphed = eng.generate(4, pos0, n, use_graph=True)
+    assert graphed == step_by_step
+    assert eng.read_position() == pos0 + n
+    np.testing.assert_array_equal(eng.logits.download(np.float32, shape.vocab), logits_eager)
+    assert eng.generate(4, pos0, n, use_graph=False) == step_by_step
     eng.close()
 
 

@@ -209,6 +209,38 @@ def test_gemm_split_from_fp32_activations(hip, oracle):
     np.testing.assert_array_equal(dc.download(np.float32, (T, M)), oracle.gemm_q8_0(w_blocks, a_blocks, NT))
 
 
+def test_gemm_split_against_asm_matmul_q8_on_fp32_activations(hip, oracle):
+    """What a caller of asm_matmul_q8 (matmul_q8_avx2.asm:51-194: int8 weights times
+    fp32 x) gets from the GEMM instead: the fp32 activations are quantized to int8
+    first, so each output differs from T calls of asm_matmul_q8 (the oracle's
+    restatement, on the unquantized rows) by the activations' rounding, at most half
+    a block step d_a = amax/127 per element: |C - ref| <= sum_k |w_k| d_a(k) / 2
+    (+ 1e-5 of the row's L1 norm for fp32 rounding).  The measured difference is
+    printed as a fraction of that bound and of the L1 norm."""
+    T, M, K = 32, 256, 2048
+    rng = np.random.default_rng(41)
+    a = rng.standard_normal((T, K)).astype(np.float32)
+    w_blocks, _ = _problem(42, 1, M, K)
+    wq, ws = oracle.split_q8_0(w_blocks)
+    da = DeviceBuffer.from_numpy(a)
+    dq, ds = DeviceBuffer(T * K), DeviceBuffer(T * K // 32 * 4)
+    dwq, dws, dc = DeviceBuffer.from_numpy(wq), DeviceBuffer.from_numpy(ws), DeviceBuffer(T * M * 4)
+    assert hip.asmhip_quantize_q8_split(da.ptr, dq.ptr, ds.ptr, T, K, None) == 0
+    assert hip.asmhip_gemm_q8_split(dwq.ptr, dws.ptr, dq.ptr, ds.ptr, dc.ptr, T, M, K, None) == 0
+    synchronize()
+    c = dc.download(np.float32, (T, M)).astype(np.float64)
+    d_a = ds.download(np.float32, (T, K // 32)).astype(np.float64)
+    wabs = np.abs(oracle.dequantize_q8_0(w_blocks).astype(np.float64))       # [M][K]
+    ref = np.stack([oracle.matmul_q8(wq, ws, a[t]) for t in range(T)]).astype(np.float64)
+    step = np.repeat(d_a, 32, axis=1) / 2                                     # [T][K]
+    bound = step @ wabs.T                                                     # sum_k |w_k| d_a(k) / 2
+    l1 = np.abs(a.astype(np.float64)) @ wabs.T
+    err = np.abs(c - ref)
+    assert np.all(err <= bound + 1e-5 * l1), f"max err / bound {np.max(err / (bound + 1e-30)):.3f}"
+    print(f"GEMM vs asm_matmul_q8 on fp32 x: max err/bound {np.max(err / bound):.3f}, "
+          f"max err/L1 {np.max(err / l1):.2e}")
+
+
 def test_gemm_split_rejects_bad_arguments(hip):
     d = DeviceBuffer(1 << 16)
     p = d.ptr

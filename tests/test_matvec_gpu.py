@@ -316,12 +316,13 @@ TILE_HEIGHT_ROWS = [1, 2, 3, 5, 16, 17, 31, 64, 100, 255, 256, 513, 1000, 1024, 
 @pytest.mark.parametrize("fmt", ["q4", "q8", "q4s", "q8s"])
 @pytest.mark.parametrize("K", [2048, 4096, 11008])
 def test_rows_do_not_depend_on_tile_height(hip, oracle, fmt, K):
-    """Below one 16-row tile per compute unit the MFMA stream cuts the rows into
-    tiles of 8, 4, 2 or 1 rows (at most one per CU), so a small matvec spreads its
-    bytes over the chip.  A row's value must not depend on the tile height: the
-    leading m rows of a 4096-row matrix (16-row tiles) give bitwise its first m
-    outputs, for every m from 1 row (1-row tiles) up; the whole matrix stays within
-    the bar of the oracle."""
+    """The MFMA stream runs 16-row tiles, and 8-row tiles (MFMA rows 8-15 loading
+    zeros) for Q8_0 and the split layouts when at most one 8-row tile falls to each
+    compute unit (M <= 2048 on 256 CUs).  A row's value must not depend on the tile
+    height or on which rows share its tile: the leading m rows of a 4096-row
+    matrix (16-row tiles) give bitwise its first m outputs, for every m from 1 up
+    (8-row tiles where the format takes them, partial tiles at ragged m); the
+    whole matrix stays within the bar of the oracle."""
     M = 4096
     blocks, x = _weights(K + len(fmt), M, K, qt=fmt[:2])
     split = fmt.endswith("s")
@@ -411,8 +412,11 @@ def test_mfma_kernel_wide_dynamic_range_of_x(hip, oracle, q4_kernel, kernel):
 def test_non_finite_x_propagates(hip, oracle, q4_kernel, qt, kernel, bad):
     """A NaN or infinite activation makes every row it touches non-finite, as
     in the reference's fp32 arithmetic: no kernel may turn it into a finite
-    number (the matrix-core kernels prepare x as fixed point and carry a NaN
-    scale for such a block)."""
+    number.  Where the fp32 sum is +-inf (an infinite x times a nonzero weight)
+    the int8-MFMA stream returns NaN instead: it prepares x as fixed point per
+    32-block and gives a block holding a NaN or an infinity a NaN scale, so an
+    infinity is not carried with its sign (a stated difference; the fp32 VALU
+    kernel keeps the reference's +-inf)."""
     q4_kernel(kernel)
     M, K = 300, 4096
     blocks, x = _weights(44, M, K, qt)
@@ -422,6 +426,13 @@ def test_non_finite_x_propagates(hip, oracle, q4_kernel, qt, kernel, bad):
         ref = oracle.matmul_q4_0_gguf(blocks, x) if qt == "q4" else oracle.matmul_q8_0_gguf(blocks, x)
     assert np.all(~np.isfinite(ref))  # the weight column at 1234 has no zero row here or NaN follows anyway
     np.testing.assert_array_equal(~np.isfinite(y), ~np.isfinite(ref))
+    mfma = kernel != native.Q4_KERNEL_FP32  # the selection applies to Q4_0 and Q8_0 alike
+    if bad == "nan" or not mfma:
+        np.testing.assert_array_equal(np.isnan(y), np.isnan(ref))
+        np.testing.assert_array_equal(y[np.isinf(ref)], ref[np.isinf(ref)])  # same infinities, same signs
+    else:
+        assert np.any(np.isinf(ref))  # the fp32 sum is +-inf on rows with a nonzero weight there
+        assert np.all(np.isnan(y))
     # the other blocks still count: a finite x with the same bytes stays finite
     x[1234] = 0.5
     assert np.all(np.isfinite(_gguf_matvec(hip, qt, blocks, x)))
