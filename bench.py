@@ -294,6 +294,115 @@ def bench_cpu_baseline(seconds: float) -> dict:
     }
 
 
+def _cpu_time(call, copies: int, seconds: float) -> tuple[float, int]:
+    """Median seconds of `call(i)` cycling over `copies` operand sets: 5 warm-ups,
+    then timed calls for `seconds` (at least 10), as bench_mt_throughput.py:82-96."""
+    for i in range(5):
+        call(i % copies)
+    times = []
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end or len(times) < 10:
+        t0 = time.perf_counter()
+        call(i % copies)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    return float(np.median(times)), len(times)
+
+
+def cpu_table_baselines(rows: list[dict], threads: int, variant: int, seconds: float = 0.5) -> dict:
+    """A CPU baseline beside every row of the matvec table: the oracle's op-for-op
+    restatement of the reference kernel for the row's format (asm_matmul_q4 AVX2 or
+    AVX-512 (`variant`), asm_matmul_q8, asm_matmul_q5 on their split planes, with the
+    threadpool's row tiling, threadpool.c:390-486, 588-665, 667-787) at the shape of
+    the row, on `threads` host threads (the headline sweep's fastest), operands rotating
+    over at least twice the host's L3.  GB/s uses the row's own algorithmic bytes, so
+    the GPU and CPU figures of a row compare the same work.  The Llama-3 layer rows
+    get the sum of their matvecs.  Annotates `rows` in place; returns the settings."""
+    from oracle import native as oracle
+
+    l3 = l3_bytes()
+    fmt_of = {name: (qt, M, K) for name, qt, M, K in MATVEC_TABLE}
+    cache: dict[tuple, float] = {}
+
+    def time_shape(qt: str, M: int, K: int) -> float:
+        fam = {"q4": "q4", "q4s": "q4", "q8": "q8", "q8s": "q8", "q5": "q5", "q5s": "q5"}[qt]
+        key = (fam, M, K)
+        if key in cache:
+            return cache[key]
+        # random planes of the format (the kernels' time does not depend on the values)
+        rng = np.random.default_rng(M * 7 + K)
+        nb = K // 32
+        x = rng.standard_normal(K, dtype=np.float32)
+        sc = rng.uniform(1e-3, 2e-3, (M, nb)).astype(np.float32)
+        if fam == "q4":
+            planes = (rng.integers(0, 256, (M, nb, 16), dtype=np.uint8), sc)
+            fn = lambda pl: oracle.matmul_q4_mt(pl[0], pl[1], x, threads, variant)  # noqa: E731
+        elif fam == "q8":
+            planes = (rng.integers(-127, 128, (M, nb, 32), dtype=np.int8), sc)
+            fn = lambda pl: oracle.matmul_q8_mt(pl[0], pl[1], x, threads)  # noqa: E731
+        else:
+            planes = (rng.integers(0, 256, (M, nb, 16), dtype=np.uint8),
+                      rng.integers(0, 256, (M, nb, 4), dtype=np.uint8), sc)
+            fn = lambda pl: oracle.matmul_q5_mt(pl[0], pl[1], pl[2], x, threads)  # noqa: E731
+        per_copy = sum(a.nbytes for a in planes)
+        copies = int(min(64, max(2, -(-2 * l3 // per_copy) if l3 else 4)))
+        sets = [planes] + [tuple(a.copy() for a in planes) for _ in range(copies - 1)]
+        med, calls = _cpu_time(lambda i: fn(sets[i]), copies, seconds)
+        cache[key] = med
+        log(f"cpu {fam} {M}x{K} on {threads} threads: {med * 1e3:.3f} ms ({copies} copies, {calls} calls)")
+        return med
+
+    kind = "asm_matmul_q4_avx512" if variant == 1 else "asm_matmul_q4"
+    names = {"q4": kind, "q4s": kind, "q8": "asm_matmul_q8", "q8s": "asm_matmul_q8", "q5": "asm_matmul_q5",
+             "q5s": "asm_matmul_q5"}
+
+    def attach(row: dict, sec: float, what: str) -> None:
+        row["cpu_baseline"] = {"us": round(sec * 1e6, 2), "GBps": round(row["bytes"] / sec / 1e9, 3),
+                               "cores": threads, "kind": "port", "sample": what,
+                               "gpu_speedup": round(sec * 1e6 / row["us"], 1)}
+
+    layer_sec = 0.0
+    for row in rows:
+        if row["op"] not in fmt_of:
+            continue
+        qt, M, K = fmt_of[row["op"]]
+        sec = time_shape(qt, M, K)
+        attach(row, sec, f"{names[qt]} restatement, {M}x{K}, split planes, threadpool row tiling")
+        if row["op"].startswith("llama3 "):
+            layer_sec += sec
+    for row in rows:
+        if row["op"].startswith("llama3 layer"):
+            attach(row, layer_sec, "sum of the 7 Llama-3 matvecs' CPU times (q, k, v, o, gate, up, down)")
+    oracle.threadpool_shutdown()
+    return {"threads": threads, "cpu_model": cpu_model(), "l3_bytes": l3, "seconds_per_shape": seconds,
+            "rotation": "operand copies >= 2x L3 per shape"}
+
+
+def cpu_gemm_baseline(gemm: dict, threads: int, T: int = 512, M: int = 11008, K: int = 4096,
+                      sample_rows: int = 16, seconds: float = 3.0) -> None:
+    """The oracle's Q8_0 GEMM (the matmul_q4_neon.S:190-255 recipe per block: int32
+    dot, product of the fp16 scales, fma, in block order) on the host threads, on a
+    bounded sample of the workload: `sample_rows` of the 512 activation rows against
+    the whole 11008x4096 weight matrix, scaled to 512 rows.  Annotates `gemm`."""
+    from asmllm_amd import gguf
+    from oracle import native as oracle
+
+    rng = np.random.default_rng(99)
+    w_blocks = gguf.quantize_q8_0(rng.standard_normal((M, K), dtype=np.float32) * np.float32(0.02))
+    a_blocks = gguf.quantize_q8_0(rng.standard_normal((sample_rows, K), dtype=np.float32))
+    med, calls = _cpu_time(lambda i: oracle.gemm_q8_0(w_blocks, a_blocks, threads), 1, seconds)
+    full = med * T / sample_rows
+    ops = 2 * T * M * K
+    oracle.threadpool_shutdown()
+    log(f"cpu GEMM {sample_rows}x{M}x{K} on {threads} threads: {med * 1e3:.1f} ms -> {full * 1e3:.1f} ms for {T} rows")
+    gemm["cpu_baseline"] = {"value": round(ops / full / 1e12, 4), "unit": "TOP/s", "us": round(full * 1e6, 1),
+                            "cores": threads, "kind": "port",
+                            "sample": f"{sample_rows} of the {T} activation rows x the {M}x{K} Q8_0 weights "
+                                      f"(oracle_gemm_q8_0, {calls} calls, median {med * 1e3:.1f} ms), scaled to {T} rows",
+                            "gpu_speedup": round(full * 1e6 / gemm["us"], 1)}
+
+
 def bench_host_pointer(seconds: float = 2.0) -> list[dict]:
     """asm_matmul_q4 as the reference's unchanged callers use it (numpy buffers in
     host memory, tests/correctness/test_runner.py:84-117, src/runtime/generate.py:255-259):
@@ -1227,6 +1336,11 @@ def main() -> None:
         extra["matvec_table"] = bench_matvec_table()
         extra["host_pointer"] = bench_host_pointer()
     cpu = None if args.no_cpu else bench_cpu_baseline(args.cpu_seconds)
+    if cpu is not None and not args.no_extra:
+        best = max(cpu["sweep"], key=lambda p: p["GBps"])
+        variant = 1 if best["kernel"] == "avx512" else 0
+        extra["cpu_table"] = cpu_table_baselines(extra["matvec_table"], best["threads"], variant)
+        cpu_gemm_baseline(extra["gemm"], best["threads"])
     traffic = None if args.no_traffic else measure_traffic()
     trace = None if args.no_trace else kernel_trace()
 
