@@ -8,10 +8,12 @@ different copy of the weights: 32 copies (813 MB) rotate, more than three
 times the 256 MB MALL, so HBM and not the last-level cache serves them.
 
 `value` is whole-job throughput: algorithmic bytes (M*(K/32)*18 + 4K + 4M per
-step) over the GPU time of exactly K steps replayed from captured HIP graphs,
-bracketed by HIP events and device synchronizations.  `roofline.achieved` uses
-the matvec kernel's average duration over that timed region (the graphs hold
-nothing else), which the rocprofv3 kernel trace of the same command matches;
+step) over the GPU time of exactly K steps (stream launches, or replays of
+captured HIP graphs past 512 steps), bracketed by HIP events and device
+synchronizations.  `roofline.achieved` uses the matvec kernel's average duration
+over that timed region (it holds nothing else) less what the two events add to
+the region on their own (timed with nothing between them); the rocprofv3 kernel
+trace of the same timed launches (`roofline.kernel_trace`) agrees with it;
 `roofline.traffic` comes from two rocprofv3 counter passes (the L2's memory read
 and write requests by size).  The CPU baseline times the oracle's restatements of
 the reference's AVX2 and AVX-512 kernels with its threadpool tiling on the host
@@ -210,6 +212,9 @@ def bench_matvec(steps: int, warmup: int, copies: int) -> dict:
         return ms, wall
 
     total_ms, wall_s = timed(steps)
+    # the same bracketing with no launch between the events: what recording the two
+    # events adds to the region (~3-4 us: a few percent of 20 steps, nothing at 4096)
+    bracket_ms = min(timed(0)[0] for _ in range(3))
     bytes_step = q4_algorithmic_bytes(M, K)
     selected = lib.asmhip_get_q4_kernel()
     # the fp32 VALU kernel on the same copies, for reference
@@ -223,7 +228,10 @@ def bench_matvec(steps: int, warmup: int, copies: int) -> dict:
         "ms_per_step": total_ms / steps,
         "steps": steps,
         "wall_s": wall_s,
-        "kernel_us_mean": total_ms * 1e3 / steps,
+        # per-launch time of the matvec over the timed region without the events'
+        # own bracketing cost (roofline.achieved); `value` keeps the whole region
+        "kernel_us_mean": max(total_ms - bracket_ms, 0.5 * total_ms) * 1e3 / steps,
+        "event_bracket_us": bracket_ms * 1e3,
         "fp32_kernel_us_mean": fp32_ms * 1e3 / n_ref,
         "bytes_per_step": bytes_step,
         "parity_max_err_over_l1": worst,
@@ -1374,6 +1382,7 @@ def main() -> None:
             "traffic_detail": traffic,
             "kernel": "gguf_mfma_stream<0,1,16,1,1> (int8 MFMA, GGUF Q4_0)",
             "kernel_us_mean": round(mv["kernel_us_mean"], 3),
+            "event_bracket_us": round(mv["event_bracket_us"], 3),
             "fp32_valu_kernel_us_mean": round(mv["fp32_kernel_us_mean"], 3),
             "bytes_per_launch": mv["bytes_per_step"],
             "kernel_trace": trace,
