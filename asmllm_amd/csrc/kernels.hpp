@@ -14,7 +14,8 @@ enum class QuantType { Q4_0, Q8_0 };
 // whether y is overwritten or accumulated into.
 enum PreOp : int {
     kPreNone = 0,
-    kPreRmsNorm = 1,  // x <- (x * 1/sqrt(mean(x^2) + eps)) * arg[k]
+    kPreRmsNorm = 1,  // x <- (x * 1/sqrt(mean(x^2) + eps)) * arg[k] (the MFMA stream: W (x * arg)
+                      // scaled by the 1/sqrt factor per row, which needs no barrier before x's digits)
     kPreSwiGlu = 2,   // x <- x / (1 + exp(-x)) * arg[k]
     // x is the decode attention output, merged from its split partials: arg is
     // the [n_heads][attn_splits][kAttnPartStride(attn_hd)] workspace that

@@ -516,6 +516,10 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         if (am_items) am.finish(&xv[0][0], &xv[0][1]);
         else xv[0][0] = xv[0][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // no item: no digit writes below
     } else if (pre == kPreRmsNorm) {
+        // RMSNorm without a barrier before the digits: y = W (inv (x * g)) =
+        // inv (W (x * g)), so x * g is digitized now and every row total is
+        // scaled by inv = 1 / sqrt(mean(x^2) + eps) after the stream, from the
+        // waves' sums of squares (read after the barrier that ends the stream)
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < XQ; ++i)
@@ -530,19 +534,14 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
             }
         ss = wave_sum(ss);
         if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        float tot = 0.f;
-#pragma unroll
-        for (int k = 0; k < NW; ++k) tot += red[k];
-        const float inv = 1.0f / sqrtf(tot / (float)K + eps);
 #pragma unroll
         for (int i = 0; i < XQ; ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                xv[i][h].x = __fmul_rn(__fmul_rn(xv[i][h].x, inv), av[i][h].x);
-                xv[i][h].y = __fmul_rn(__fmul_rn(xv[i][h].y, inv), av[i][h].y);
-                xv[i][h].z = __fmul_rn(__fmul_rn(xv[i][h].z, inv), av[i][h].z);
-                xv[i][h].w = __fmul_rn(__fmul_rn(xv[i][h].w, inv), av[i][h].w);
+                xv[i][h].x = __fmul_rn(xv[i][h].x, av[i][h].x);
+                xv[i][h].y = __fmul_rn(xv[i][h].y, av[i][h].y);
+                xv[i][h].z = __fmul_rn(xv[i][h].z, av[i][h].z);
+                xv[i][h].w = __fmul_rn(xv[i][h].w, av[i][h].w);
             }
     } else if (pre == kPreSwiGlu) {
 #pragma unroll
@@ -684,7 +683,15 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     }
     __syncthreads();
 
-    // 5) add the waves' partial sums of every row in a fixed order.
+    // 5) add the waves' partial sums of every row in a fixed order (RMSNorm:
+    // then scale the total by inv).
+    float inv = 1.f;
+    if (!AM && pre == kPreRmsNorm) {
+        float tot = 0.f;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) tot += red[k];
+        inv = 1.0f / sqrtf(tot / (float)K + eps);
+    }
     if (post == kPostSwiGlu8) {
         // a tile is 8 gate rows and their 8 up rows (M % 16 == 0, TH = 16): y[8 tile + r] = silu(gate) * up
         for (int idx = threadIdx.x; idx < my_tiles * 8; idx += kThreads) {
@@ -696,6 +703,8 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
                 gs += part[(i * NW + k) * 16 + r];
                 us += part[(i * NW + k) * 16 + 8 + r];
             }
+            gs = __fmul_rn(gs, inv);
+            us = __fmul_rn(us, inv);
             y[tile * 8 + r] = __fmul_rn(gs / (1.0f + expf(-gs)), us);
         }
         return;
@@ -707,6 +716,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
             float sum = 0.f;
 #pragma unroll
             for (int k = 0; k < NW; ++k) sum += part[(i * NW + k) * 16 + r];
+            sum = __fmul_rn(sum, inv);
             y[row] = accumulate ? y[row] + sum : sum;
         }
     }

@@ -53,7 +53,10 @@ extern "C" {
 
 /* Work fused into a matvec's read of x (asmhip_matmul_fused). */
 #define ASMHIP_PRE_NONE 0
-#define ASMHIP_PRE_RMSNORM 1 /* x <- (x * 1/sqrt(mean(x^2) + eps)) * pre_arg */
+#define ASMHIP_PRE_RMSNORM 1 /* x <- (x * 1/sqrt(mean(x^2) + eps)) * pre_arg (the int8-MFMA stream
+                                * reads x * pre_arg and scales each row total by the
+                                * 1/sqrt factor: the same product, rounded in another
+                                * order, within the matvec bar) */
 #define ASMHIP_PRE_SWIGLU 2  /* x <- x / (1 + exp(-x)) * pre_arg             */
 
 /* Matvec kernel selection (asmhip_set_q4_kernel): the int8-MFMA stream or the
