@@ -365,12 +365,16 @@ __device__ __forceinline__ float tile_total(float acc) {
 // fixed number of loads per wave so the wait for them does not also wait for
 // the weights.
 template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH>
+// Argument order: what the prologue reads before the first weight loads comes
+// first (the leading kernel-argument dwords arrive preloaded in SGPRs; a later
+// one would cost a kernel-argument load in front of the weight stream).
 __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __restrict__ w,
+                                                            const float* __restrict__ x,
+                                                            const float* __restrict__ pre_arg,
                                                             const uint8_t* __restrict__ wh,
-                                                            const float* __restrict__ wsc,
-                                                            const float* __restrict__ x, float* __restrict__ y,
-                                                            int M, int K, int pre, const float* __restrict__ pre_arg,
-                                                            float eps, int accumulate, int post, int pre_hd) {
+                                                            const float* __restrict__ wsc, int M, int K, int pre,
+                                                            float* __restrict__ y, float eps, int accumulate,
+                                                            int post, int pre_hd) {
     using U = Unit<QT>;
     constexpr int kThreads = NW * 64;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -747,7 +751,7 @@ int launch_xq(const Planes& pw, const float* x, float* y, int M, int K, int grid
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
     hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH>), dim3(grid), dim3(NW * 64), lds, st, pw.w,
-                       pw.wh, pw.wsc, x, y, M, K, o.pre, o.pre_arg, o.eps, (int)o.accumulate, o.post, o.attn_hd);
+                       x, o.pre_arg, pw.wh, pw.wsc, M, K, o.pre, y, o.eps, (int)o.accumulate, o.post, o.attn_hd);
     return kOk;
 }
 
