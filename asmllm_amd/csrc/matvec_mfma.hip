@@ -363,11 +363,13 @@ __device__ __forceinline__ float tile_total(float acc) {
 // (kPreAttnMerge: heads of pre_hd dimensions, pre_hd % 32 == 0, one x item per
 // thread); the states are requested before the weight stream, as x is, with a
 // fixed number of loads per wave so the wait for them does not also wait for
-// the weights.
-template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH>
+// the weights.  RP (accumulate launches): each workgroup's rows of y are read
+// right after the first weight loads are issued, so y += W x does not wait for
+// a read of y after the stream.
 // Argument order: what the prologue reads before the first weight loads comes
 // first (the leading kernel-argument dwords arrive preloaded in SGPRs; a later
 // one would cost a kernel-argument load in front of the weight stream).
+template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH, bool RP>
 __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ pre_arg,
@@ -499,6 +501,14 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
 #pragma unroll
     for (int d = 0; d < D; ++d) load_unit(buf[d], d);
     __builtin_amdgcn_sched_barrier(0);
+    // the residual rows this thread adds to (one row at most: my_tiles * 16 <= the threads)
+    float resid = 0.f;
+    if constexpr (RP) {
+        static_assert(kMaxTilesPerGroup * 16 <= kThreads, "one stored row per thread");
+        const int i = (int)threadIdx.x >> 4, r = (int)threadIdx.x & 15;
+        const int row = ((int)blockIdx.x + G * i) * TH + r;
+        if ((int)threadIdx.x < my_tiles * 16 && r < TH && row < M) resid = y[row];
+    }
 
     // 3) fused pre-op on x, then digits; partial sums start at zero.
     for (int i = threadIdx.x; i < my_tiles * NW * 16; i += kThreads) part[i] = 0.f;
@@ -721,7 +731,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
 #pragma unroll
             for (int k = 0; k < NW; ++k) sum += part[(i * NW + k) * 16 + r];
             sum = __fmul_rn(sum, inv);
-            y[row] = accumulate ? y[row] + sum : sum;
+            y[row] = RP ? resid + sum : accumulate ? y[row] + sum : sum;
         }
     }
 }
@@ -744,15 +754,29 @@ struct Planes {
     const float* wsc;
 };
 
+template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH, bool RP>
+int launch_rp(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
+              const MatvecOpts& o) {
+    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH, RP>;
+    const int rc = dynamic_lds(fn, lds);
+    if (rc) return rc;
+    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH, RP>), dim3(grid), dim3(NW * 64), lds, st,
+                       pw.w, x, o.pre_arg, pw.wh, pw.wsc, M, K, o.pre, y, o.eps, (int)o.accumulate, o.post,
+                       o.attn_hd);
+    return kOk;
+}
+
+// Q4_0 accumulate launches whose waves stream several units per tile (PW = 0:
+// K != 4096, the decode engine's down projection) take the kernel that reads
+// its residual rows early (4096x11008 / 4096x14336: 9.38 -> 9.20 us); with one
+// unit per wave (K = 4096) the early read measured slower (4.68 -> 4.93 us) and
+// the rows are read after the stream.
 template <int QT, int XQ, int NW, int D, int PW, int AMS = 0, bool NTW = false, int TH = 16>
 int launch_xq(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
-    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH>;
-    const int rc = dynamic_lds(fn, lds);
-    if (rc) return rc;
-    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH>), dim3(grid), dim3(NW * 64), lds, st, pw.w,
-                       x, o.pre_arg, pw.wh, pw.wsc, M, K, o.pre, y, o.eps, (int)o.accumulate, o.post, o.attn_hd);
-    return kOk;
+    if constexpr (QT == kFmtQ4_0 && PW == 0)
+        if (o.accumulate) return launch_rp<QT, XQ, NW, D, PW, AMS, NTW, TH, true>(pw, x, y, M, K, grid, lds, st, o);
+    return launch_rp<QT, XQ, NW, D, PW, AMS, NTW, TH, false>(pw, x, y, M, K, grid, lds, st, o);
 }
 
 // x items (8 positions) per thread -> the matching instantiation
