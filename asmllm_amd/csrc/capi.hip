@@ -733,6 +733,12 @@ extern "C" int asmhip_stream_read_shaped(const void* buf, int64_t bytes, const f
                               (hipStream_t)stream);
 }
 
+extern "C" int asmhip_matmul_q4_0_stamped(const void* blocks, const float* x, float* y, int64_t M, int64_t K,
+                                          uint64_t* stamps, int64_t stamps_len, void* stream) {
+    if (!blocks || !x || !y) return fail(kInvalidArgument, "null pointer argument");
+    return q4_0_mfma_stamped_launch(blocks, x, y, M, K, stamps, stamps_len, (hipStream_t)stream);
+}
+
 extern "C" int asmhip_empty_launch(int grid, int threads, int lds, void* stream) {
     return empty_launch(grid, threads, lds, (hipStream_t)stream);
 }

@@ -66,6 +66,10 @@ int get_q4_kernel();
 bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& opts, int64_t M, int64_t K);
 int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t stream,
                      const MatvecOpts& opts);
+// Measurement: the headline Q4_0 launch (K = 4096, M > 2048) with every wave
+// recording 8 real-time stamps (100 MHz) into stamps[(block * 16 + wave) * 8 + i].
+int q4_0_mfma_stamped_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, uint64_t* stamps,
+                             int64_t stamps_len, hipStream_t stream);
 // The same stream over 22-byte GGUF Q5_0 blocks (no fused pre-ops).
 bool q5_0_mfma_eligible(const void* w, const float* x, int64_t M, int64_t K);
 int q5_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t stream);

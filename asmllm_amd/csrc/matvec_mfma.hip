@@ -369,14 +369,25 @@ __device__ __forceinline__ float tile_total(float acc) {
 // Argument order: what the prologue reads before the first weight loads comes
 // first (the leading kernel-argument dwords arrive preloaded in SGPRs; a later
 // one would cost a kernel-argument load in front of the weight stream).
-template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH, bool RP>
+// ST (measurement only): every wave records the 100 MHz real-time counter at
+// kStampCount points of its life into stamps[(block * NW + wave) * kStampCount + i].
+constexpr int kStampCount = 8;
+template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH, bool RP, bool ST = false>
 __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ pre_arg,
                                                             const uint8_t* __restrict__ wh,
                                                             const float* __restrict__ wsc, int M, int K, int pre,
                                                             float* __restrict__ y, float eps, int accumulate,
-                                                            int post, int pre_hd) {
+                                                            int post, int pre_hd, uint64_t* __restrict__ stamps) {
+    // stamps: 0 entry, 1 first weight loads issued, 2 x digits ready (after the
+    // barrier), 3 first unit landed, 4 last unit landed, 5 stream done, 6 all
+    // waves done (after the barrier), 7 y stored and its writes complete
+    uint64_t stv[ST ? kStampCount : 1];
+    auto mark = [&](int i) {
+        if constexpr (ST) stv[i] = __builtin_amdgcn_s_memrealtime();
+    };
+    mark(0);
     using U = Unit<QT>;
     constexpr int kThreads = NW * 64;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -501,6 +512,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
 #pragma unroll
     for (int d = 0; d < D; ++d) load_unit(buf[d], d);
     __builtin_amdgcn_sched_barrier(0);
+    mark(1);
     // the residual rows this thread adds to (one row at most: my_tiles * 16 <= the threads)
     float resid = 0.f;
     if constexpr (RP) {
@@ -622,6 +634,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         }
     }
     __syncthreads();
+    mark(2);
 
     // 4) the stream: stage unit s, multiply, refill its buffer with unit s + D.
     constexpr int kPairs = kUnitBlocks / 2;
@@ -655,6 +668,10 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
                     if (q < U::kPieces) park_piece<QT>(wbuf, q, buf[d][k]);
                 }
                 __builtin_amdgcn_wave_barrier();
+                if constexpr (ST) {
+                    if (s == 0) mark(3);
+                    if (s == L - 1) mark(4);
+                }
                 // the unit is parked: refill its registers before the compute,
                 // so the next unit's latency overlaps this unit's MFMAs
                 load_unit(buf[d], s + D);
@@ -695,7 +712,9 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
             }
         }
     }
+    mark(5);
     __syncthreads();
+    mark(6);
 
     // 5) add the waves' partial sums of every row in a fixed order (RMSNorm:
     // then scale the total by inv).
@@ -734,6 +753,12 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
             y[row] = RP ? resid + sum : accumulate ? y[row] + sum : sum;
         }
     }
+    if constexpr (ST) {
+        __builtin_amdgcn_s_waitcnt(0);  // the y stores complete
+        mark(7);
+        if (lane == 0)
+            for (int i = 0; i < kStampCount; ++i) stamps[((size_t)blockIdx.x * NW + wave) * kStampCount + i] = stv[i];
+    }
 }
 
 // Launch shapes.  The wide shape runs 16 waves with one unit of loads in
@@ -762,7 +787,7 @@ int launch_rp(const Planes& pw, const float* x, float* y, int M, int K, int grid
     if (rc) return rc;
     hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH, RP>), dim3(grid), dim3(NW * 64), lds, st,
                        pw.w, x, o.pre_arg, pw.wh, pw.wsc, M, K, o.pre, y, o.eps, (int)o.accumulate, o.post,
-                       o.attn_hd);
+                       o.attn_hd, nullptr);
     return kOk;
 }
 
@@ -941,6 +966,29 @@ bool q4_0_mfma_eligible(const void* w, const float* x, const MatvecOpts& o, int6
 int q4_0_mfma_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, hipStream_t st,
                      const MatvecOpts& o) {
     return mfma_launch<kFmtQ4_0>(Planes{static_cast<const uint8_t*>(w), nullptr, nullptr}, x, y, M, K, st, o);
+}
+
+int q4_0_mfma_stamped_launch(const void* w, const float* x, float* y, int64_t M, int64_t K, uint64_t* stamps,
+                             int64_t stamps_len, hipStream_t st) {
+    using U = Unit<kFmtQ4_0>;
+    const Planes pw{static_cast<const uint8_t*>(w), nullptr, nullptr};
+    const MatvecOpts o;
+    const StreamShape sh = stream_shape(U::kSlotBytes, M, K);
+    // the headline launch shape only: K = 4096, 16 waves with their x operands in
+    // registers, 16-row tiles, plain loads (M > 2048)
+    if (!mfma_eligible<kFmtQ4_0>(pw, x, o, M, K) || K != 16 * 256 || sh.waves != kWideWaves || (M + 15) / 16 <= 128)
+        return fail(kUnsupported, "stamped matvec: only Q4_0 K = 4096, M > 2048 (the headline launch shape)");
+    if (!stamps || stamps_len < (int64_t)sh.grid * kWideWaves * kStampCount)
+        return fail(kInvalidArgument, "stamped matvec: stamps needs %lld entries",
+                    (long long)sh.grid * kWideWaves * kStampCount);
+    const void* fn = (const void*)gguf_mfma_stream<kFmtQ4_0, 1, kWideWaves, kWideDepth, 1, 0, false, 16, false, true>;
+    const int rc = dynamic_lds(fn, sh.lds);
+    if (rc) return rc;
+    hipLaunchKernelGGL((gguf_mfma_stream<kFmtQ4_0, 1, kWideWaves, kWideDepth, 1, 0, false, 16, false, true>),
+                       dim3(sh.grid), dim3(kWideWaves * 64), sh.lds, st, pw.w, x, o.pre_arg, pw.wh, pw.wsc, (int)M,
+                       (int)K, o.pre, y, o.eps, 0, o.post, o.attn_hd, stamps);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
 }
 
 bool q5_0_mfma_eligible(const void* w, const float* x, int64_t M, int64_t K) {

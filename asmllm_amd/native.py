@@ -82,6 +82,7 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_stream_read": (c_int, [_P, c_int64, _P, _P]),
     "asmhip_stream_read_shaped": (c_int, [_P, c_int64, _P, c_int, _P, c_int64, c_int, c_int, _P, _P]),
     "asmhip_empty_launch": (c_int, [c_int, c_int, c_int, _P]),
+    "asmhip_matmul_q4_0_stamped": (c_int, [_P, _P, _P, c_int64, c_int64, _P, c_int64, _P]),
     "asmhip_grid_barrier": (c_int, [_P, c_int, _P, _P]),
     "asmhip_attention_decode_noalloc_max_floats": (c_int64, []),
     "asmhip_attention_decode_rope_noalloc": (c_int, [_P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, c_float, _P]),

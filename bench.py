@@ -743,6 +743,94 @@ def bench_read_floor(multiples=(1, 2, 4, 8)) -> dict:
             "grid_barrier": bench_grid_barrier(cus)}
 
 
+STAMP_EVENTS = ("entry", "first weight loads issued", "x digits ready", "first unit landed", "last unit landed",
+                "stream done", "all waves done", "y written")
+
+
+def bench_stamps(launches: int = 64, copies: int = 32) -> dict:
+    """Where one 11008x4096 launch spends its time, from inside the kernel: the
+    headline matvec in its stamped instantiation (asmhip_matmul_q4_0_stamped: every
+    wave records the 100 MHz real-time counter at 8 points), `launches` back-to-back
+    launches replayed from one graph over rotating weight copies behind untimed
+    cover reads.  Per event: percentiles over all waves of the time since the
+    launch's first wave started; per launch: the span from the first wave's start to
+    the last wave's completed y write, and the gap from there to the next launch's
+    first wave.  The stamps cost time of their own (their scalar reads of the
+    counter and stores): the stamped and plain launches are timed side by side."""
+    from asmllm_amd import native
+    from asmllm_amd.device import DeviceBuffer, Event, Graph, Stream, synchronize
+
+    lib = native.lib()
+    M, K = M_MAIN, K_MAIN
+    bufs, _ = _rotating_blocks(native.Q4_0, M, K, copies, seed=7)
+    x, y, y2 = DeviceBuffer(4 * K), DeviceBuffer(4 * M), DeviceBuffer(4 * M)
+    native.check(lib.asmhip_fill_f32(x.ptr, K, 0.5, None), "fill")
+    grid = min((M + 15) // 16, device_info_cus())
+    per = grid * 16 * len(STAMP_EVENTS)
+    st_buf = DeviceBuffer(8 * per * launches)
+    cov, sink = DeviceBuffer(1 << 30), DeviceBuffer(4096)
+    stream = Stream()
+
+    def stamped(i: int) -> None:
+        native.check(lib.asmhip_matmul_q4_0_stamped(bufs[i % copies].ptr, x.ptr, y.ptr, M, K, st_buf.ptr + 8 * per * i,
+                                                    per, stream.handle), "stamped matvec")
+
+    def plain(i: int) -> None:
+        native.check(lib.asmhip_matmul_q4_0(bufs[i % copies].ptr, x.ptr, y2.ptr, M, K, stream.handle), "matvec")
+
+    stamped(0)
+    plain(0)
+    stream.synchronize()
+    same = bool(np.array_equal(y.download(np.uint32, M), y2.download(np.uint32, M)))
+    g_st = Graph.capture(stream, lambda: [stamped(i) for i in range(launches)])
+    g_pl = Graph.capture(stream, lambda: [plain(i) for i in range(launches)])
+    e0, e1 = Event(timing=True), Event(timing=True)
+
+    def timed(g) -> float:
+        g.launch(stream)
+        synchronize()
+        for _ in range(200):  # ~30 ms of untimed reads: the GPU busy while the graph is queued
+            native.check(lib.asmhip_stream_read(cov.ptr, cov.nbytes, sink.ptr, stream.handle), "cover")
+        e0.record(stream)
+        g.launch(stream)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) * 1e3 / launches
+
+    t_pl = min(timed(g_pl) for _ in range(3))
+    t_st = min(timed(g_st) for _ in range(3))
+    a = st_buf.download(np.uint64, (launches, grid * 16, len(STAMP_EVENTS))).astype(np.int64)
+    g_st.close()
+    g_pl.close()
+    first = a[:, :, 0].min(axis=1)
+    last = a[:, :, -1].max(axis=1)
+    rel = (a - first[:, None, None]) * 0.01  # 100 MHz ticks -> us
+    keep = slice(4, launches)  # the first launches of a replay start the stream
+    events = []
+    for i, name in enumerate(STAMP_EVENTS):
+        v = rel[keep, :, i]
+        v = v[a[keep, :, i] > 0]
+        events.append({"event": name, "p10_us": round(float(np.percentile(v, 10)), 3),
+                       "median_us": round(float(np.median(v)), 3), "p90_us": round(float(np.percentile(v, 90)), 3),
+                       "max_us": round(float(v.max()), 3)})
+    span = (last - first)[keep] * 0.01
+    gap = (first[1:] - last[:-1])[keep.start:] * 0.01
+    tiles = -(-((M + 15) // 16 - np.arange(grid)) // grid)
+    wg_end = rel[keep, :, -1].reshape(-1, grid, 16).max(axis=2)
+    by_tiles = {int(t): round(float(np.median(wg_end[:, tiles == t])), 3) for t in sorted(set(tiles.tolist()))}
+    for b in bufs:
+        b.close()
+    log(f"stamps: plain {t_pl:.3f} us/launch, stamped {t_st:.3f}; span {span.mean():.3f}, gap {gap.mean():.3f}")
+    return {"workload": f"Q4_0 matvec {M}x{K}, {launches} back-to-back launches from one graph, {copies} weight copies",
+            "kernel": "gguf_mfma_stream<0,1,16,1,1,0,false,16> (stamped instantiation)",
+            "stamped_y_bitwise_equal_plain": same,
+            "plain_us_per_launch": round(t_pl, 3), "stamped_us_per_launch": round(t_st, 3),
+            "events_us_since_first_wave": events,
+            "span_us_mean": round(float(span.mean()), 3), "gap_us_mean": round(float(gap.mean()), 3),
+            "gap_us_min": round(float(gap.min()), 3),
+            "workgroup_end_median_us_by_tiles": by_tiles}
+
+
 def device_info_cus() -> int:
     from asmllm_amd.device import device_info
 
@@ -1299,7 +1387,7 @@ def main() -> None:
     ap.add_argument("--no-trace", action="store_true", help="skip the rocprofv3 kernel trace of the timed region")
     ap.add_argument("--no-extra", action="store_true", help="skip the shape table, GEMM and decode legs")
     ap.add_argument("--only", choices=["decode", "gemm", "table", "floor", "host", "cpu", "traffic", "gemm_counters",
-                                       "phases", "trace"],
+                                       "phases", "trace", "stamps"],
                     help="run one extra leg and print its JSON")
     ap.add_argument("--eager", action="store_true", help="with --only: launch without graphs")
     args = ap.parse_args()
@@ -1328,7 +1416,7 @@ def main() -> None:
             res = {"gemm": bench_gemm, "table": bench_matvec_table, "floor": bench_read_floor,
                    "host": bench_host_pointer, "traffic": measure_traffic,
                    "gemm_counters": gemm_counters, "phases": bench_matvec_phases,
-                   "trace": kernel_trace}[args.only]()
+                   "trace": kernel_trace, "stamps": bench_stamps}[args.only]()
         print(json.dumps({args.only: res}), flush=True)
         return
 

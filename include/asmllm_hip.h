@@ -295,6 +295,14 @@ ASMHIP_API int asmhip_stream_read(const void* buf, int64_t bytes, void* sink, vo
  * end.  `sink` is 4 KB of device memory. */
 ASMHIP_API int asmhip_stream_read_shaped(const void* buf, int64_t bytes, const float* x, int xn, float* y,
                                          int64_t y_floats, int flags, int lds, void* sink, void* stream);
+/* Measurement (no counterpart in the reference): asmhip_matmul_q4_0 at its headline
+ * launch shape (K = 4096, M > 2048) in an instantiation where every wave records
+ * the 100 MHz real-time counter at 8 points (entry, first weight loads issued, x
+ * digits ready, first unit landed, last unit landed, stream done, all waves done,
+ * y written) into stamps[(workgroup * 16 + wave) * 8 + i] (device memory, at least
+ * workgroups * 128 entries: min(ceil(M / 16), CUs) workgroups).  Same y. */
+ASMHIP_API int asmhip_matmul_q4_0_stamped(const void* blocks, const float* x, float* y, int64_t M, int64_t K,
+                                          uint64_t* stamps, int64_t stamps_len, void* stream);
 /* Measurement (no counterpart in the reference): an empty kernel of `grid`
  * workgroups of `threads` threads with `lds` bytes of dynamic LDS. */
 ASMHIP_API int asmhip_empty_launch(int grid, int threads, int lds, void* stream);
