@@ -23,10 +23,11 @@
 // one 32x32 tile on the coalesced path below (4 waves of two on the general
 // path: wave (wt, wm) owns rows 32 wt.. and columns 64 wm..).
 // Fast path (K % 64 == 0): K goes in steps of two blocks; a row's step is 68
-// contiguous bytes, fetched with 16-byte loads by consecutive lanes and parked
-// raw in LDS (row pitch an odd number of dwords: conflict-free operand reads),
-// double-buffered with the next step's loads in flight.  Other K: blocks are
-// staged one by one with qs realigned on the way into LDS.
+// contiguous bytes, fetched as the 16-byte aligned 80-byte window around them
+// with 16-byte loads by consecutive lanes and parked raw in LDS (two stages side
+// by side in each row, row stride an odd number of dwords: conflict-free operand
+// reads), with the next two steps' loads in flight.  Other K: blocks are staged
+// one by one with qs realigned on the way into LDS.
 // gemm_q8_split takes the split operands of asm_matmul_q8 (int8 qs planes and
 // fp32 scale planes) with the same tiling; see its comment.
 #include <type_traits>
@@ -202,59 +203,72 @@ __global__ __launch_bounds__(kThreadsG) void gemm_q8_0_kernel(const uint8_t* __r
 }
 
 // ---------------------------------------------------------------------------
-// Coalesced variant (K % 128 == 0): a step's K chunk of a row is KB * 34
-// contiguous bytes, fetched with 16-byte loads by consecutive lanes and parked
-// raw in LDS at a row pitch of an odd number of dwords (lanes of a 32-row
-// operand read land in distinct banks).  Operands are realigned as they are
-// read: qs of an even block start 2 bytes past a dword.
+// Coalesced variant (K % 64 == 0): a step's K chunk of a row is KB * 34
+// contiguous bytes, fetched with aligned 16-byte loads by consecutive lanes and
+// parked raw in LDS; a row's two stages sit side by side and rows are an odd
+// number of dwords apart (lanes of a 32-row operand read land in distinct
+// banks).  The even block's qs start 2 bytes past a dword and are read in
+// another order of k (raw_qs).
 // ---------------------------------------------------------------------------
-template <int KB, int NTH>
+template <int KB, int NTH, int TT, int TM>
 struct RawStep {
     static constexpr int kChunk = KB * 34;                        // bytes of a row's K chunk
-    static constexpr int kPieces = (kChunk + 15) / 16;            // 16-byte loads per row
-    static constexpr int kPitch = ((kPieces * 16 / 4) | 1) * 4;   // odd number of dwords
-    static constexpr int kRows = kTT + kTM;
+    static constexpr int kPieces = (kChunk + 12 + 15) / 16;       // 16-byte loads per row (the chunk starts
+                                                                  // up to 12 bytes into its aligned window)
+    static constexpr int kStageOff = kPieces * 16;                // stage 1 of a row follows stage 0
+    static constexpr int kRowStride = ((2 * kStageOff / 4) | 1) * 4;  // odd number of dwords
+    static constexpr int kRows = TT + TM;
     static constexpr int kTotal = kRows * kPieces;
     static constexpr int kPerThread = (kTotal + NTH - 1) / NTH;
-    static constexpr int kStage = kRows * kPitch + 16;             // + spare dwords for dead slots
+    static constexpr int kBytes = kRows * kRowStride + 2 * kStageOff;  // + a dead slot's landing place
 };
 
-// 16 qs bytes of block BLK (of a dword-aligned pair) for lane group g: an odd
-// block's qs are dword aligned, an even block's start 2 bytes past a dword
+// 16 qs bytes of block BLK (of a dword-aligned pair) for lane group g.  The odd
+// block's qs are dword aligned.  The even block's start 2 bytes past a dword,
+// after its scale: lane group g reads the pair's aligned dwords 4g..4g+3, and
+// group 0 (selector 0x07060100; group 1 passes 0x07060504, the identity) puts
+// q30 and q31, the low half of dword 8, in place of the scale's two bytes.  The
+// 32 qs then sit in another order of k than the block's, the same order for A
+// and W, so the int32 dot is unchanged.
 template <int BLK>
-__device__ __forceinline__ v4i raw_qs(const uint8_t* row, int g) {
-    constexpr int off = 34 * BLK + 2;
-    const uint8_t* p = row + 16 * g;
-    if constexpr (off % 4 == 0) {
-        const uint32_t* d = reinterpret_cast<const uint32_t*>(p + off);
+__device__ __forceinline__ v4i raw_qs(const uint8_t* row, int g, uint32_t sel) {
+    if constexpr (BLK == 1) {
+        const uint32_t* d = reinterpret_cast<const uint32_t*>(row + 36 + 16 * g);
         return v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
     } else {
-        const uint32_t* d = reinterpret_cast<const uint32_t*>(p + off - 2);
-        const uint32_t w0 = d[0], w1 = d[1], w2 = d[2], w3 = d[3], w4 = d[4];
-        return v4i{(int)__builtin_amdgcn_alignbyte(w1, w0, 2), (int)__builtin_amdgcn_alignbyte(w2, w1, 2),
-                   (int)__builtin_amdgcn_alignbyte(w3, w2, 2), (int)__builtin_amdgcn_alignbyte(w4, w3, 2)};
+        const uint32_t* d = reinterpret_cast<const uint32_t*>(row + 16 * g);
+        const uint32_t tail = *reinterpret_cast<const uint32_t*>(row + 32);
+        return v4i{(int)__builtin_amdgcn_perm(d[0], tail, sel), (int)d[1], (int)d[2], (int)d[3]};
     }
 }
 
 // A 32x32x8 f16 MFMA operand holding the block's raw fp16 scale in its first
-// half: with the scale in both lane halves of A and B, D = 2 d_a d_w exactly.
+// half (the 16-bit LDS read zero-extends): with the scale in both lane halves
+// of A and B, D = 2 d_a d_w exactly.
 template <int BLK>
 __device__ __forceinline__ v4h raw_scale(const uint8_t* row) {
-    v4h v = {};
-    v[0] = *reinterpret_cast<const _Float16*>(row + 34 * BLK);
-    return v;
+    typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+    uint32_t d = *reinterpret_cast<const uint16_t*>(row + 34 * BLK);
+    asm("" : "+v"(d));  // an opaque dword: the pair is built without masking the high half again
+    return __builtin_bit_cast(v4h, (v2u){d, 0u});
 }
 
-// WT = 32-column tiles per wave: 2 -> 4 waves of 32x64 (256 threads),
-// 1 -> 8 waves of 32x32 (512 threads, twice the waves to hide each wave's
-// MFMA -> epilogue latency).
-template <int KB, int D, int WT>
-__global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* __restrict__ w,
+// A workgroup computes a TT x TM tile with (TT / 32) x (TM / (32 WT)) waves,
+// each of WT 32x32 tiles side by side (WT = 1: one tile a wave, twice the waves
+// of WT = 2 to hide each wave's MFMA -> epilogue latency).  Two K steps of
+// loads in flight per thread.  The loop body is written once for each step of
+// a four-step cycle (stage s % 2, window shift 4 (s % 4) bytes), so every LDS
+// address is a per-lane base plus a constant.  The register budget is held to
+// six waves per SIMD (80 VGPRs).
+template <int KB, int WT, int TT, int TM>
+__global__ __launch_bounds__(TT * TM / (16 * WT)) __attribute__((amdgpu_waves_per_eu(6))) void gemm_q8_0_coalesced(const uint8_t* __restrict__ w,
                                                                const uint8_t* __restrict__ a,
                                                                float* __restrict__ c, int T, int M, int K,
                                                                int tiles_t, int n_tiles) {
-    constexpr int NTH = 512 / WT, MW = 4 / WT;  // threads; waves along M
-    using S = RawStep<KB, NTH>;
+    constexpr int MW = TM / (32 * WT), NTH = (TT / 32) * MW * 64;  // waves along M; threads
+    using S = RawStep<KB, NTH, TT, TM>;
+    static_assert(TT * S::kPieces % 64 == 0 && NTH % 64 == 0, "every wave's load slot is all A or all W");
+    static_assert(KB == 2, "a step's window shift 4 (s % 4) holds for 68-byte steps");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     // XCD-aware tile order: workgroup ids are dealt round-robin to the 8 XCDs,
     // so id -> (xcd = id % 8, j = id / 8) -> tile xcd * chunk + j gives each XCD
@@ -265,12 +279,11 @@ __global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* _
     if (tile >= n_tiles) return;
     const int nb = K >> 5;
     const uint32_t row_bytes = (uint32_t)nb * 34u;
-    const int t0 = (tile % tiles_t) * kTT, j0 = (tile / tiles_t) * kTM;
+    const uint32_t a_bytes = row_bytes * (uint32_t)T, w_bytes = row_bytes * (uint32_t)M;
+    const int t0 = (tile % tiles_t) * TT, j0 = (tile / tiles_t) * TM;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wt = wave / MW, wm = wave % MW;
-    const auto ar = make_rsrc(a, row_bytes * (uint32_t)T);
-    const auto wr = make_rsrc(w, row_bytes * (uint32_t)M);
 
     // piece q = (staged row q / kPieces, 16-byte piece q % kPieces); A rows first.
     // Slots past the last piece load from past the buffer (zeros, no access) and
@@ -283,26 +296,31 @@ __global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* _
         const bool live = q < S::kTotal;
         const int qq = live ? q : 0;
         const int r = qq / S::kPieces, k = qq - r * S::kPieces;
-        is_a[i] = r < kTT;
-        const int grow = is_a[i] ? t0 + r : j0 + (r - kTT);
+        is_a[i] = r < TT;
+        const int grow = is_a[i] ? t0 + r : j0 + (r - TT);
         goff[i] = live ? (uint32_t)grow * row_bytes + 16u * (uint32_t)k : kPastEnd;
-        loff[i] = live ? (uint32_t)(r * S::kPitch + 16 * k) : (uint32_t)(S::kRows * S::kPitch);
+        loff[i] = live ? (uint32_t)(r * S::kRowStride + 16 * k) : (uint32_t)(S::kRows * S::kRowStride);
     }
-    uint4 pre[D][S::kPerThread];
-    // A's pieces end at piece 64 kPieces, a multiple of 64, and NTH is a multiple
+    uint4 pre[2][S::kPerThread];  // two steps of loads in flight
+    // A's pieces end at piece TT kPieces, a multiple of 64, and NTH is a multiple
     // of 64, so every wave's slot i is all A or all W: the choice of buffer is
     // wave-uniform (made scalar here; a per-lane choice of descriptor would turn
     // every load into a waterfall loop).
     bool a_wave[S::kPerThread];
 #pragma unroll
     for (int i = 0; i < S::kPerThread; ++i) a_wave[i] = __builtin_amdgcn_readfirstlane((int)is_a[i]) != 0;
+    // Step s of a row is the 16-byte aligned window of 80 bytes holding its 68
+    // (kb0 * 34 rounded down to 16: the window starts 4 (s % 4) bytes early), so
+    // every 16-byte load is aligned.  The window's offset goes into the
+    // descriptors (base advanced, size cut by the same amount): the per-slot
+    // offsets stay fixed, and the range check still ends at each buffer's last
+    // byte (a window that runs past it reads zeros for the dwords beyond).
     auto fetch = [&](uint4* dst, int kb0) {
-        const uint32_t kofs = (uint32_t)kb0 * 34u;
+        const uint32_t kofs = ((uint32_t)kb0 * 34u) & ~15u;
+        const auto ar = make_rsrc(a + kofs, a_bytes - kofs);
+        const auto wr = make_rsrc(w + kofs, w_bytes - kofs);
 #pragma unroll
-        for (int i = 0; i < S::kPerThread; ++i) {
-            const uint32_t off = goff[i] == kPastEnd ? kPastEnd : goff[i] + kofs;
-            dst[i] = buf_load_b128(a_wave[i] ? ar : wr, off);
-        }
+        for (int i = 0; i < S::kPerThread; ++i) dst[i] = buf_load_b128(a_wave[i] ? ar : wr, goff[i]);
     };
     auto park = [&](const uint4* src, uint8_t* stage) {
 #pragma unroll
@@ -316,6 +334,7 @@ __global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* _
     };
 
     const int m = lane & 31, g = lane >> 5;
+    const uint32_t sel = g ? 0x07060504u : 0x07060100u;
     v16f acc[WT];
 #pragma unroll
     for (int nt = 0; nt < WT; ++nt)
@@ -323,58 +342,68 @@ __global__ __launch_bounds__(512 / WT) void gemm_q8_0_coalesced(const uint8_t* _
         for (int i = 0; i < 16; ++i) acc[nt][i] = 0.f;
 
     const int nsteps = nb / KB;
+    fetch(pre[0], 0);
+    fetch(pre[1], min(1, nsteps - 1) * KB);
+    // step s parks in stage s % 2 of every row; its data start 4 (s % 4) bytes
+    // into the stage.  Both stages of a row sit side by side, so one base
+    // address per row serves both with offsets the LDS instructions carry.
+    auto step = [&](auto s4_c, int s) {
+        constexpr int S4 = decltype(s4_c)::value;
+        uint8_t* stage = lds + (S4 & 1) * S::kStageOff;
+        park(pre[S4 & 1], stage);
+        __syncthreads();
+        // unconditional, so the loop body stays one basic block: the last two
+        // steps load the last step again, into registers that are never parked
+        fetch(pre[S4 & 1], min(s + 2, nsteps - 1) * KB);
+        const uint8_t* arow = stage + (32 * wt + m) * S::kRowStride + 4 * S4;
+        const uint8_t* wrow = stage + (TT + 32 * WT * wm + m) * S::kRowStride + 4 * S4;
+        // block BLK (0 or 1) of the dword-aligned pair at byte 68 bp: operands,
+        // then the matrix instructions back to back, then the epilogue
+        auto block = [&](auto blk_c, int bp) {
+            constexpr int BLK = decltype(blk_c)::value;
+            const uint8_t* ar_ = arow + 68 * bp;
+            const v4i av = raw_qs<BLK>(ar_, g, sel);
+            const v4h da = raw_scale<BLK>(ar_);
+            v4i bv[WT];
+            v4h dw[WT];
 #pragma unroll
-    for (int u = 0; u < D; ++u)
-        if (u < nsteps) fetch(pre[u], u * KB);
-    for (int s0 = 0; s0 < nsteps; s0 += D) {
-#pragma unroll
-        for (int u = 0; u < D; ++u) {
-            const int s = s0 + u;
-            if (s >= nsteps) break;
-            uint8_t* stage = lds + (s & 1) * S::kStage;
-            park(pre[u], stage);
-            __syncthreads();
-            if (s + D < nsteps) fetch(pre[u], (s + D) * KB);
-            const uint8_t* arow = stage + (32 * wt + m) * S::kPitch;
-            const uint8_t* wrow = stage + (kTT + 32 * WT * wm + m) * S::kPitch;
-            // block BLK (0 or 1) of the dword-aligned pair at byte 68 bp: operands,
-            // then the matrix instructions back to back, then the epilogue
-            auto block = [&](auto blk_c, int bp) {
-                constexpr int BLK = decltype(blk_c)::value;
-                const uint8_t* ar_ = arow + 68 * bp;
-                const v4i av = raw_qs<BLK>(ar_, g);
-                const v4h da = raw_scale<BLK>(ar_);
-                v4i bv[WT];
-                v4h dw[WT];
-#pragma unroll
-                for (int nt = 0; nt < WT; ++nt) {
-                    const uint8_t* w_ = wrow + 32 * nt * S::kPitch + 68 * bp;
-                    bv[nt] = raw_qs<BLK>(w_, g);
-                    dw[nt] = raw_scale<BLK>(w_);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                const v16i zi = {};
-                const v16f zf = {};
-                v16i dd[WT];
-                v16f ss[WT];
-#pragma unroll
-                for (int nt = 0; nt < WT; ++nt) {
-                    dd[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[nt], zi, 0, 0, 0);
-                    ss[nt] = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw[nt], zf, 0, 0, 0);  // 2 d_a d_w
-                }
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int nt = 0; nt < WT; ++nt)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) acc[nt][i] = fmaf((float)dd[nt][i], ss[nt][i], acc[nt][i]);
-            };
-#pragma unroll 1
-            for (int bp = 0; bp < KB / 2; ++bp) {
-                block(std::integral_constant<int, 0>{}, bp);
-                block(std::integral_constant<int, 1>{}, bp);
+            for (int nt = 0; nt < WT; ++nt) {
+                const uint8_t* w_ = wrow + 32 * nt * S::kRowStride + 68 * bp;
+                bv[nt] = raw_qs<BLK>(w_, g, sel);
+                dw[nt] = raw_scale<BLK>(w_);
             }
+            __builtin_amdgcn_sched_barrier(0);
+            const v16i zi = {};
+            const v16f zf = {};
+            v16i dd[WT];
+            v16f ss[WT];
+#pragma unroll
+            for (int nt = 0; nt < WT; ++nt) {
+                dd[nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[nt], zi, 0, 0, 0);
+                ss[nt] = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw[nt], zf, 0, 0, 0);  // 2 d_a d_w
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int nt = 0; nt < WT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[nt][i] = fmaf((float)dd[nt][i], ss[nt][i], acc[nt][i]);
+        };
+#pragma unroll
+        for (int bp = 0; bp < KB / 2; ++bp) {
+            block(std::integral_constant<int, 0>{}, bp);
+            block(std::integral_constant<int, 1>{}, bp);
         }
+    };
+    int s = 0;
+    for (; s + 3 < nsteps; s += 4) {
+        step(std::integral_constant<int, 0>{}, s);
+        step(std::integral_constant<int, 1>{}, s + 1);
+        step(std::integral_constant<int, 2>{}, s + 2);
+        step(std::integral_constant<int, 3>{}, s + 3);
     }
+    if (s < nsteps) step(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+    if (s + 2 < nsteps) step(std::integral_constant<int, 2>{}, s + 2);
 
 #pragma unroll
     for (int nt = 0; nt < WT; ++nt) {
@@ -519,12 +548,16 @@ __global__ __launch_bounds__(kSplitThreads) void gemm_q8_split(const int8_t* __r
     }
 }
 
-// Two blocks per staged K step, one step of loads in flight per thread.
-// Deeper register rings (2-4 steps) and 4- or 8-block steps measured slower on
-// MI355X: the extra registers cost occupancy.  So did issuing both blocks'
-// matrix instructions before either epilogue (194 VGPRs with two tiles a wave).
+// Two blocks per staged K step, two steps of loads in flight per thread, at
+// 80 VGPRs: six waves per SIMD, so three 8-wave workgroups share a compute unit.
+// Deeper rings and 4- or 8-block steps cost occupancy on MI355X, and so did
+// issuing both blocks' matrix instructions before either epilogue (194 VGPRs
+// with two tiles a wave).  Workgroup tiles of 128 x 96 (12 waves) and 64 x 192
+// measured slower than 64 x 128 at 512 x 11008 x 4096 (101.8 and 87.6 us
+// against 85.2).
 constexpr int kGemmKB = 2;  // blocks per staged K step (even)
-constexpr int kGemmD = 1;   // K steps of loads in flight per thread
+constexpr int kCoTT = 64;   // T rows per workgroup tile of the coalesced kernel
+constexpr int kCoTM = 128;  // M columns per workgroup tile of the coalesced kernel
 constexpr int kGemmWT = 1;  // 32-column tiles per wave: 8 waves of one tile (4 of two measured 4% slower)
 
 }  // namespace
@@ -534,19 +567,20 @@ int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t 
         return fail(kInvalidArgument, "gemm: need T, M, K > 0 and K %% 32 == 0 (got T=%lld M=%lld K=%lld)",
                     (long long)T, (long long)M, (long long)K);
     const int64_t row_bytes = K / 32 * 34;
-    if ((T + kTT) * row_bytes >= (int64_t)kPastEnd || (M + kTM) * row_bytes >= (int64_t)kPastEnd)
+    if ((T + 128) * row_bytes >= (int64_t)kPastEnd || (M + 256) * row_bytes >= (int64_t)kPastEnd)
         return fail(kInvalidArgument, "gemm: operands above 4 GB are not supported");
     if ((uintptr_t)w % 4 || (uintptr_t)a % 4) return fail(kInvalidArgument, "gemm: blocks must be 4-byte aligned");
     const dim3 grid((unsigned)((M + kTM - 1) / kTM), (unsigned)((T + kTT - 1) / kTT));
     if (grid.y > 65535) return fail(kInvalidArgument, "gemm: T too large");
     if ((K / 32) % kGemmKB == 0) {
-        const int tiles_t = (int)grid.y, n_tiles = (int)(grid.x * grid.y);
+        const int tiles_t = (int)((T + kCoTT - 1) / kCoTT), n_tiles = tiles_t * (int)((M + kCoTM - 1) / kCoTM);
         const unsigned padded = (unsigned)((n_tiles + 7) / 8 * 8);
-        constexpr int kThreads = 512 / kGemmWT;
-        const size_t lds = 2 * (size_t)RawStep<kGemmKB, kThreads>::kStage;
-        const int rc = dynamic_lds((const void*)gemm_q8_0_coalesced<kGemmKB, kGemmD, kGemmWT>, lds);
+        constexpr int kThreads = kCoTT * kCoTM / (16 * kGemmWT);
+        const size_t lds = (size_t)RawStep<kGemmKB, kThreads, kCoTT, kCoTM>::kBytes;
+        const auto kern = gemm_q8_0_coalesced<kGemmKB, kGemmWT, kCoTT, kCoTM>;
+        const int rc = dynamic_lds((const void*)kern, lds);
         if (rc) return rc;
-        hipLaunchKernelGGL((gemm_q8_0_coalesced<kGemmKB, kGemmD, kGemmWT>), dim3(padded), dim3(kThreads), lds, st,
+        hipLaunchKernelGGL(kern, dim3(padded), dim3(kThreads), lds, st,
                            static_cast<const uint8_t*>(w), static_cast<const uint8_t*>(a), c, (int)T, (int)M, (int)K,
                            tiles_t, n_tiles);
     } else {
