@@ -521,6 +521,33 @@ extern "C" int asmhip_gemm_q8_0(const void* w_blocks, const void* a_blocks, floa
     return rc ? rc : gemm_q8_0_launch(w_blocks, a_blocks, c, T, M, K, (hipStream_t)stream);
 }
 
+extern "C" int64_t asmhip_gemm_q8_0_tiled_weight_bytes(int64_t M, int64_t K) {
+    return M > 0 && K > 0 && K % 64 == 0 ? gemm_tiled_bytes(M, K, kGemmTileW) : 0;
+}
+
+extern "C" int64_t asmhip_gemm_q8_0_tiled_activation_bytes(int64_t T, int64_t K) {
+    return T > 0 && K > 0 && K % 64 == 0 ? gemm_tiled_bytes(T, K, kGemmTileA) : 0;
+}
+
+extern "C" int asmhip_gemm_q8_0_tile_weights(const void* w_blocks, void* w_tiled, int64_t M, int64_t K,
+                                             void* stream) {
+    return gemm_tile_blocks_launch(w_blocks, w_tiled, M, K, kGemmTileW, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_gemm_q8_0_tile_activations(const void* a_blocks, void* a_tiled, int64_t T, int64_t K,
+                                                 void* stream) {
+    return gemm_tile_blocks_launch(a_blocks, a_tiled, T, K, kGemmTileA, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_quantize_q8_0_tiled(const float* x, void* a_tiled, int64_t T, int64_t K, void* stream) {
+    return quantize_q8_0_tiled_launch(x, a_tiled, T, K, (hipStream_t)stream);
+}
+
+extern "C" int asmhip_gemm_q8_0_tiled(const void* w_tiled, const void* a_tiled, float* c, int64_t T, int64_t M,
+                                      int64_t K, void* stream) {
+    return gemm_q8_0_tiled_launch(w_tiled, a_tiled, c, T, M, K, (hipStream_t)stream);
+}
+
 extern "C" int asmhip_gemm_q8_split(const int8_t* w_qs, const float* w_scales, const int8_t* a_qs,
                                     const float* a_scales, float* c, int64_t T, int64_t M, int64_t K, void* stream) {
     int rc = check_ptrs(w_qs, a_qs, c);

@@ -417,6 +417,161 @@ __global__ __launch_bounds__(TT * TM / (16 * WT)) __attribute__((amdgpu_waves_pe
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Tiled variant: the operands in the GEMM tile layout (gemm_tiled_offset), so a
+// workgroup's K step is one contiguous run per operand: TT rows x 68 bytes of A
+// and TM rows x 68 bytes of W.  Each wave's 16-byte buffer loads write LDS
+// themselves (buffer_load_dwordx4 ... lds: lane i lands at M0 + 16 i), so a
+// run lands as it lies: rows 68 bytes (17 dwords, odd) apart, conflict-free
+// operand reads, no staging registers and no LDS write instructions.  Three
+// stages, two steps in flight.  The compiler cannot tell the stages apart for
+// its own LDS-DMA wait bookkeeping (it would wait for every load in flight
+// before each LDS read), so the loads are issued from inline asm and each step
+// waits by count for its own loads only (s_waitcnt vmcnt), then a bare barrier.
+// ---------------------------------------------------------------------------
+template <int TT, int TM>
+struct DmaStep {
+    static constexpr int kARegion = (TT * 68 + 1023) / 1024 * 1024;  // A rows, padded to whole 1 KB loads
+    static constexpr int kWRegion = (TM * 68 + 1023) / 1024 * 1024;
+    static constexpr int kLoads = (kARegion + kWRegion) / 1024;      // wave-wide 1 KB loads per step
+    static constexpr int kALoads = kARegion / 1024;
+    static constexpr int kStage = kARegion + kWRegion + 1024;         // + the landing place of padding loads
+};
+
+// The dwords of a raw buffer descriptor (base, stride 0, size; word 3 as
+// make_rsrc), for use as an asm operand.
+__device__ __forceinline__ v4i raw_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t p = (uint64_t)base;
+    return v4i{(int)(uint32_t)p, (int)(uint32_t)((p >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
+}
+
+template <int TT, int TM>
+__global__ __launch_bounds__(TT * TM / 16) __attribute__((amdgpu_waves_per_eu(6))) void gemm_q8_0_tiled(
+    const uint8_t* __restrict__ w, const uint8_t* __restrict__ a, float* __restrict__ c, int T, int M, int K,
+    int tiles_t, int n_tiles) {
+    constexpr int MW = TM / 32, NW = (TT / 32) * MW;  // waves along M; waves
+    using S = DmaStep<TT, TM>;
+    constexpr int kPerWave = (S::kLoads + NW - 1) / NW;  // loads each wave issues per step (padding ones too)
+    __shared__ __attribute__((aligned(1024))) uint8_t st0[S::kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t st1[S::kStage];
+    __shared__ __attribute__((aligned(1024))) uint8_t st2[S::kStage];
+    // XCD-aware tile order, as gemm_q8_0_coalesced
+    const int chunk = (int)gridDim.x >> 3;
+    const int tile = ((int)blockIdx.x & 7) * chunk + ((int)blockIdx.x >> 3);
+    if (tile >= n_tiles) return;
+    const int nsteps = K >> 6;
+    const int tt = tile % tiles_t, tm = tile / tiles_t;
+    const int t0 = tt * TT, j0 = tm * TM;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wt = wave / MW, wm = wave % MW;
+    const uint8_t* abase = a + (size_t)tt * nsteps * (TT * 68);
+    const uint8_t* wbase = w + (size_t)tm * nsteps * (TM * 68);
+    // Step s into stage ST: load j = wave + NW u of the step's 1 KB loads, A's
+    // first; loads past the last one read past the buffer (zeros, no access)
+    // into the stage's spare kilobyte, so every wave issues kPerWave.
+    auto fetch = [&](auto stage_c, int s) {
+        constexpr int ST = decltype(stage_c)::value;
+        uint8_t* stage = ST == 0 ? st0 : ST == 1 ? st1 : st2;
+        const v4i ar = raw_rsrc(abase + (size_t)s * (TT * 68), TT * 68);
+        const v4i wr = raw_rsrc(wbase + (size_t)s * (TM * 68), TM * 68);
+#pragma unroll
+        for (int u = 0; u < kPerWave; ++u) {
+            const int j = wave + NW * u;  // wave-uniform
+            const bool is_a = j < S::kALoads, pad = j >= S::kLoads;
+            const int jj = is_a ? j : j - S::kALoads;
+            uint8_t* dst = stage + (pad ? S::kARegion + S::kWRegion : is_a ? 1024 * jj : S::kARegion + 1024 * jj);
+            const uint32_t off = pad ? kPastEnd : (uint32_t)(1024 * jj + 16 * lane);
+            const uint32_t m0 = (uint32_t)(size_t)(__attribute__((address_space(3))) void*)dst;
+            const v4i rs = is_a ? ar : wr;
+            // M0 is the only LDS-DMA operand the builtin would set; this kernel has
+            // no other M0 user (no compiler-issued LDS DMA, no movrel indexing), so
+            // clobbering it here, which clang warns of in general, is safe
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+            asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(m0), "s"(rs)
+                         : "memory", "m0");
+#pragma clang diagnostic pop
+        }
+    };
+    const int m = lane & 31, g = lane >> 5;
+    const uint32_t sel = g ? 0x07060504u : 0x07060100u;
+    v16f acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    fetch(std::integral_constant<int, 0>{}, 0);
+    fetch(std::integral_constant<int, 1>{}, min(1, nsteps - 1));
+    auto step = [&](auto stage_c, int s) {
+        constexpr int ST = decltype(stage_c)::value;
+        const uint8_t* stage = ST == 0 ? st0 : ST == 1 ? st1 : st2;
+        // this wave's loads of step s have landed once at most those of step
+        // s + 1 are outstanding (vmcnt <= kPerWave; expcnt, lgkmcnt not waited)
+        __builtin_amdgcn_s_waitcnt(0xF70 | kPerWave);
+        __builtin_amdgcn_s_barrier();
+        // stage (s + 2) % 3 was read by step s - 1, which every wave finished
+        // before the barrier; past the end the last step is loaded again
+        fetch(std::integral_constant<int, (ST + 2) % 3>{}, min(s + 2, nsteps - 1));
+        const uint8_t* arow = stage + (32 * wt + m) * 68;
+        const uint8_t* wrow = stage + S::kARegion + (32 * wm + m) * 68;
+        auto block = [&](auto blk_c) {
+            constexpr int BLK = decltype(blk_c)::value;
+            const v4i av = raw_qs<BLK>(arow, g, sel);
+            const v4h da = raw_scale<BLK>(arow);
+            const v4i bv = raw_qs<BLK>(wrow, g, sel);
+            const v4h dw = raw_scale<BLK>(wrow);
+            __builtin_amdgcn_sched_barrier(0);
+            const v16i zi = {};
+            const v16f zf = {};
+            const v16i dd = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, zi, 0, 0, 0);
+            const v16f ss = __builtin_amdgcn_mfma_f32_32x32x8f16(da, dw, zf, 0, 0, 0);  // 2 d_a d_w
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = fmaf((float)dd[i], ss[i], acc[i]);
+        };
+        block(std::integral_constant<int, 0>{});
+        block(std::integral_constant<int, 1>{});
+    };
+    int s = 0;
+    for (; s + 2 < nsteps; s += 3) {
+        step(std::integral_constant<int, 0>{}, s);
+        step(std::integral_constant<int, 1>{}, s + 1);
+        step(std::integral_constant<int, 2>{}, s + 2);
+    }
+    if (s < nsteps) step(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < nsteps) step(std::integral_constant<int, 1>{}, s + 1);
+    __builtin_amdgcn_s_waitcnt(0xF70);  // no wave ends with loads into LDS in flight
+    const int col = j0 + 32 * wm + m;
+    if (col < M) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = t0 + 32 * wt + 8 * (i / 4) + 4 * g + i % 4;
+            if (row < T) c[(size_t)row * M + col] = 0.5f * acc[i];  // the scales entered doubled
+        }
+    }
+}
+
+// GGUF Q8_0 rows -> the GEMM tile layout: one thread per (tile, step, row)
+// run of 68 bytes (17 dwords); rows past the last one are zero.
+__global__ __launch_bounds__(256) void gemm_tile_blocks_kernel(const uint32_t* __restrict__ src,
+                                                               uint32_t* __restrict__ dst, int64_t rows,
+                                                               int64_t padded_rows, int nb, int R) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // run index in tiled order
+    const int64_t nsteps = nb / 2;
+    if (i >= padded_rows * nsteps) return;
+    const int64_t row_in = i % R, step = (i / R) % nsteps, tile = i / (R * nsteps);
+    const int64_t row = tile * R + row_in;
+    uint32_t* d = dst + i * 17;
+    if (row < rows) {
+        const uint32_t* s = src + (row * nb * 34 + step * 68) / 4;  // nb even: dword aligned
+#pragma unroll
+        for (int k = 0; k < 17; ++k) d[k] = s[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < 17; ++k) d[k] = 0u;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Split-layout variant: int8 qs planes [rows][K] and fp32 scale planes
 // [rows][K/32], the operand layout of the reference's asm_matmul_q8
@@ -613,6 +768,37 @@ int gemm_q8_split_launch(const int8_t* wq, const float* wsc, const int8_t* aq, c
     if (rc) return rc;
     hipLaunchKernelGGL(gemm_q8_split, dim3(padded), dim3(kSplitThreads), lds, st, wq, wsc, aq, asc, c, (int)T, (int)M,
                        (int)K, (int)tiles_t, (int)n_tiles);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int gemm_q8_0_tiled_launch(const void* w_tiled, const void* a_tiled, float* c, int64_t T, int64_t M, int64_t K,
+                           hipStream_t st) {
+    if (T <= 0 || M <= 0 || K <= 0 || K % 64)
+        return fail(kInvalidArgument, "gemm_tiled: need T, M, K > 0 and K %% 64 == 0 (got T=%lld M=%lld K=%lld)",
+                    (long long)T, (long long)M, (long long)K);
+    if (!w_tiled || !a_tiled || !c) return fail(kInvalidArgument, "gemm_tiled: null pointer");
+    if ((uintptr_t)w_tiled % 16 || (uintptr_t)a_tiled % 16)
+        return fail(kInvalidArgument, "gemm_tiled: operands must be 16-byte aligned");
+    const int64_t tiles_t = (T + kGemmTileA - 1) / kGemmTileA, n_tiles = tiles_t * ((M + kGemmTileW - 1) / kGemmTileW);
+    if (n_tiles > (1 << 24)) return fail(kInvalidArgument, "gemm_tiled: T x M too large");
+    const unsigned padded = (unsigned)((n_tiles + 7) / 8 * 8);
+    hipLaunchKernelGGL((gemm_q8_0_tiled<kGemmTileA, kGemmTileW>), dim3(padded), dim3(kGemmTileA * kGemmTileW / 16), 0, st,
+                       static_cast<const uint8_t*>(w_tiled), static_cast<const uint8_t*>(a_tiled), c, (int)T, (int)M,
+                       (int)K, (int)tiles_t, (int)n_tiles);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int gemm_tile_blocks_launch(const void* blocks, void* tiled, int64_t rows, int64_t K, int R, hipStream_t st) {
+    if (rows <= 0 || K <= 0 || K % 64) return fail(kInvalidArgument, "gemm tiling: need rows > 0 and K %% 64 == 0");
+    if (!blocks || !tiled || (uintptr_t)blocks % 4 || (uintptr_t)tiled % 4)
+        return fail(kInvalidArgument, "gemm tiling: null or unaligned buffer");
+    const int64_t padded = (rows + R - 1) / R * R, runs = padded * (K / 64);
+    if ((runs + 255) / 256 > INT32_MAX) return fail(kInvalidArgument, "gemm tiling: tensor too large");
+    hipLaunchKernelGGL(gemm_tile_blocks_kernel, dim3((unsigned)((runs + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const uint32_t*>(blocks), static_cast<uint32_t*>(tiled), rows, padded,
+                       (int)(K / 32), R);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

@@ -88,6 +88,24 @@ int split_mfma_launch(int bits, const void* qs, const uint8_t* qh, const float* 
 // C[T][M] = A (Q8_0 blocks [T][K/32]) x W (Q8_0 blocks [M][K/32])^T, block dots
 // scaled by both fp16 scales and accumulated in block order.
 int gemm_q8_0_launch(const void* w, const void* a, float* c, int64_t T, int64_t M, int64_t K, hipStream_t stream);
+
+// GEMM tile layout of Q8_0 blocks: rows in tiles of R (kGemmTileA = 64 for the
+// activations, kGemmTileW = 128 for the weights), the tiles one after another,
+// within a tile the K steps of two blocks, within a step the tile's rows, 68
+// bytes each (the two blocks as they lie in the GGUF row).  Rows past the last
+// one pad the last tile.  K % 64 == 0.
+constexpr int kGemmTileA = 64;
+constexpr int kGemmTileW = 128;
+__host__ __device__ inline int64_t gemm_tiled_offset(int64_t row, int64_t blk, int64_t nb, int R) {
+    return ((row / R * (nb / 2) + blk / 2) * R + row % R) * 68 + (blk % 2) * 34;
+}
+__host__ __device__ inline int64_t gemm_tiled_bytes(int64_t rows, int64_t K, int R) {
+    return (rows + R - 1) / R * R * (K / 32) * 34;
+}
+int gemm_q8_0_tiled_launch(const void* w_tiled, const void* a_tiled, float* c, int64_t T, int64_t M, int64_t K,
+                           hipStream_t stream);
+int gemm_tile_blocks_launch(const void* blocks, void* tiled, int64_t rows, int64_t K, int R, hipStream_t stream);
+int quantize_q8_0_tiled_launch(const float* x, void* tiled, int64_t rows, int64_t K, hipStream_t stream);
 int gemm_q8_split_launch(const int8_t* wq, const float* wsc, const int8_t* aq, const float* asc, float* c, int64_t T,
                          int64_t M, int64_t K, hipStream_t stream);
 

@@ -94,6 +94,19 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(const float* __restr
         quant_q4_block(v, out + i * 18);
 }
 
+// The same Q8_0 blocks written in the GEMM tile layout of activations
+// (gemm_tiled_offset with kGemmTileA-row tiles); padding rows are not written.
+__global__ __launch_bounds__(kThreads) void quantize_q8_tiled_kernel(const float* __restrict__ w,
+                                                                     uint8_t* __restrict__ out, int64_t nblocks,
+                                                                     int64_t nb) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= nblocks) return;
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = w[i * 32 + j];
+    quant_q8_block(v, out + gemm_tiled_offset(i / nb, i % nb, nb, kGemmTileA));
+}
+
 // The split layout of the same blocks: qs[i] = the 32 quants of block i
 // (16-byte aligned), scales[i] = its fp16 d widened to fp32.
 __global__ __launch_bounds__(kThreads) void quantize_q8_split_kernel(const float* __restrict__ w, int8_t* __restrict__ qs,
@@ -190,6 +203,17 @@ int quantize_q8_split_launch(const float* w, int8_t* qs, float* scales, int64_t 
     const int64_t nb = rows * (K / 32);
     if (grid_for(nb) > INT32_MAX) return fail(kInvalidArgument, "quantize_q8_split: tensor too large");
     hipLaunchKernelGGL(quantize_q8_split_kernel, dim3((unsigned)grid_for(nb)), dim3(kThreads), 0, st, w, qs, scales, nb);
+    ASMHIP_TRY(hipGetLastError());
+    return kOk;
+}
+
+int quantize_q8_0_tiled_launch(const float* x, void* tiled, int64_t rows, int64_t K, hipStream_t st) {
+    if (rows <= 0 || K <= 0 || K % 64) return fail(kInvalidArgument, "quantize_q8_0_tiled: need rows > 0 and K %% 64 == 0");
+    if (!x || !tiled) return fail(kInvalidArgument, "quantize_q8_0_tiled: null pointer");
+    const int64_t nb = rows * (K / 32);
+    if (grid_for(nb) > INT32_MAX) return fail(kInvalidArgument, "quantize_q8_0_tiled: tensor too large");
+    hipLaunchKernelGGL(quantize_q8_tiled_kernel, dim3((unsigned)grid_for(nb)), dim3(kThreads), 0, st, x,
+                       (uint8_t*)tiled, nb, K / 32);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
 }

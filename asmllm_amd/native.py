@@ -59,6 +59,12 @@ SIGNATURES: dict[str, tuple] = {
     "asmhip_matmul_swiglu": (c_int, [c_int, _P, _P, _P, c_int64, c_int64, c_int, _P, c_float, _P, _P]),
     "asmhip_gemm_q8_0": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, _P]),
     "asmhip_gemm_q8_split": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P]),
+    "asmhip_gemm_q8_0_tiled_weight_bytes": (c_int64, [c_int64, c_int64]),
+    "asmhip_gemm_q8_0_tiled_activation_bytes": (c_int64, [c_int64, c_int64]),
+    "asmhip_gemm_q8_0_tile_weights": (c_int, [_P, _P, c_int64, c_int64, _P]),
+    "asmhip_gemm_q8_0_tile_activations": (c_int, [_P, _P, c_int64, c_int64, _P]),
+    "asmhip_quantize_q8_0_tiled": (c_int, [_P, _P, c_int64, c_int64, _P]),
+    "asmhip_gemm_q8_0_tiled": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, _P]),
     "asmhip_set_q4_kernel": (c_int, [c_int]),
     "asmhip_get_q4_kernel": (c_int, []),
     "asmhip_quantize": (c_int, [c_int, _P, _P, c_int64, c_int64, _P]),

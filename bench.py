@@ -929,9 +929,13 @@ INT8_MFMA_PEAK_TOPS = 5000.0
 
 def bench_gemm(T: int = 512, M: int = 11008, K: int = 4096, copies: int = 12) -> dict:
     """Q8_0 x Q8_0 prefill GEMM: activations 512x4096 fp32 quantized per row on
-    the GPU, weights 11008x4096 Q8_0; ops = 2*T*M*K."""
+    the GPU, weights 11008x4096 Q8_0; ops = 2*T*M*K.  The headline form takes
+    both operands in the GEMM tile layout (the same Q8_0 blocks, permuted): the
+    weights arranged once (a load-time cost, reported, not timed per call), the
+    activations quantized straight into it.  The GGUF-block form and the split
+    form are timed on the same blocks."""
     from asmllm_amd import gguf, native
-    from asmllm_amd.device import DeviceBuffer
+    from asmllm_amd.device import DeviceBuffer, Event, Stream
 
     lib = native.lib()
     wbufs, _ = _rotating_blocks(native.Q8_0, M, K, copies, seed=99)
@@ -941,17 +945,42 @@ def bench_gemm(T: int = 512, M: int = 11008, K: int = 4096, copies: int = 12) ->
     native.check(lib.asmhip_random_blocks(native.Q8_0, dq.ptr, T, K, 5, 1.0, None), "random activations")
     dc = DeviceBuffer(4 * T * M)
 
+    # the tile layout: weights arranged once per copy, activations from the same blocks
+    wt_bytes = lib.asmhip_gemm_q8_0_tiled_weight_bytes(M, K)
+    wtiled = [DeviceBuffer(wt_bytes) for _ in range(copies)]
+    st = Stream()
+    e0, e1 = Event(timing=True), Event(timing=True)
+    e0.record(st)
+    native.check(lib.asmhip_gemm_q8_0_tile_weights(wbufs[0].ptr, wtiled[0].ptr, M, K, st.handle), "tile weights")
+    e1.record(st)
+    e1.synchronize()
+    tile_us = e0.elapsed_ms(e1) * 1e3
+    for b in wtiled[1:]:
+        b.copy_from(wtiled[0])
+    dqt = DeviceBuffer(lib.asmhip_gemm_q8_0_tiled_activation_bytes(T, K))
+    native.check(lib.asmhip_gemm_q8_0_tile_activations(dq.ptr, dqt.ptr, T, K, None), "tile activations")
+
+    def gemm_tiled(i, st):
+        native.check(lib.asmhip_gemm_q8_0_tiled(wtiled[i % copies].ptr, dqt.ptr, dc.ptr, T, M, K, st), "gemm tiled")
+
+    def quant_tiled(i, st):
+        native.check(lib.asmhip_quantize_q8_0_tiled(da.ptr, dqt.ptr, T, K, st), "quantize tiled")
+
     def gemm(i, st):
         native.check(lib.asmhip_gemm_q8_0(wbufs[i % copies].ptr, dq.ptr, dc.ptr, T, M, K, st), "gemm")
 
     def quant(i, st):
         native.check(lib.asmhip_quantize(native.Q8_0, da.ptr, dq.ptr, T, K, st), "quantize")
 
-    us = time_launches(gemm, copies, reps=20)
+    us = time_launches(gemm_tiled, copies, reps=20)
+    us_qt = time_launches(quant_tiled, copies, reps=20)
+    # restore the random activation blocks the other forms use
+    native.check(lib.asmhip_gemm_q8_0_tile_activations(dq.ptr, dqt.ptr, T, K, None), "tile activations")
+    us_b = time_launches(gemm, copies, reps=20)
     us_q = time_launches(quant, copies, reps=20)
     ops = 2 * T * M * K
     nbytes = gguf.q8_0_nbytes(M, K) + gguf.q8_0_nbytes(T, K) + 4 * T * M
-    log(f"GEMM {T}x{M}x{K}: {us:.2f} us, {ops / us / 1e6:.0f} TOP/s")
+    log(f"GEMM {T}x{M}x{K} tile layout: {us:.2f} us, {ops / us / 1e6:.0f} TOP/s; GGUF blocks: {us_b:.2f} us")
 
     # the same operands in the split layout (int8 qs planes + fp32 scale planes);
     # the results are bitwise those of the block-form GEMM
@@ -974,14 +1003,19 @@ def bench_gemm(T: int = 512, M: int = 11008, K: int = 4096, copies: int = 12) ->
     us_s = time_launches(gemm_split, copies, reps=20)
     nbytes_s = M * K + 4 * M * nb + T * K + 4 * T * nb + 4 * T * M
     log(f"GEMM split layout: {us_s:.2f} us, {ops / us_s / 1e6:.0f} TOP/s")
-    return {"workload": f"Q8_0 GEMM C[{T}][{M}] = A_q8[{T}][{K}] . W_q8[{M}][{K}]^T", "us": round(us, 3),
-            "TOPs": round(ops / us / 1e6, 1), "frac_int8_mfma_peak": round(ops / us / 1e6 / INT8_MFMA_PEAK_TOPS, 4),
-            "GBps": round(nbytes / us / 1e3, 1), "activation_quantize_us": round(us_q, 3), "ops": ops,
-            "bytes": nbytes,
+
+    def form(us_, nbytes_):
+        return {"us": round(us_, 3), "TOPs": round(ops / us_ / 1e6, 1),
+                "frac_int8_mfma_peak": round(ops / us_ / 1e6 / INT8_MFMA_PEAK_TOPS, 4), "bytes": nbytes_}
+
+    return {"workload": f"Q8_0 GEMM C[{T}][{M}] = A_q8[{T}][{K}] . W_q8[{M}][{K}]^T, operands in the GEMM tile "
+                        f"layout (the same Q8_0 blocks; weights arranged once, activations quantized into it)",
+            **form(us, nbytes), "GBps": round(nbytes / us / 1e3, 1), "ops": ops,
+            "activation_quantize_us": round(us_qt, 3), "weight_tiling_us_once": round(tile_us, 3),
+            "block_layout": {"layout": "GGUF Q8_0 blocks [rows][K/32] as given (asmhip_gemm_q8_0)",
+                             **form(us_b, nbytes), "activation_quantize_us": round(us_q, 3)},
             "split_layout": {"layout": "int8 qs [rows][K] + fp32 scales [rows][K/32] (asm_matmul_q8's operands)",
-                             "us": round(us_s, 3), "TOPs": round(ops / us_s / 1e6, 1),
-                             "frac_int8_mfma_peak": round(ops / us_s / 1e6 / INT8_MFMA_PEAK_TOPS, 4),
-                             "bytes": nbytes_s}}
+                             **form(us_s, nbytes_s)}}
 
 
 def decode_cpu_baseline(eng, context: int, seconds: float) -> dict:
@@ -1290,6 +1324,18 @@ def gemm_profile_pass(T: int = 512, M: int = 11008, K: int = 4096, copies: int =
     native.check(lib.asmhip_random_blocks(native.Q8_0, dq.ptr, T, K, 5, 1.0, None), "random activations")
     dc = DeviceBuffer(4 * T * M)
     stream = Stream()
+    # the tile layout (the headline form)
+    wtiled = [DeviceBuffer(lib.asmhip_gemm_q8_0_tiled_weight_bytes(M, K)) for _ in range(copies)]
+    for b, wt in zip(wbufs, wtiled):
+        native.check(lib.asmhip_gemm_q8_0_tile_weights(b.ptr, wt.ptr, M, K, stream.handle), "tile weights")
+    dqt = DeviceBuffer(lib.asmhip_gemm_q8_0_tiled_activation_bytes(T, K))
+    native.check(lib.asmhip_gemm_q8_0_tile_activations(dq.ptr, dqt.ptr, T, K, stream.handle), "tile activations")
+    for i in range(launches):
+        native.check(lib.asmhip_gemm_q8_0_tiled(wtiled[i % copies].ptr, dqt.ptr, dc.ptr, T, M, K, stream.handle),
+                     "gemm tiled")
+    stream.synchronize()
+    for b in wtiled:
+        b.close()
     for i in range(launches):
         native.check(lib.asmhip_gemm_q8_0(wbufs[i % copies].ptr, dq.ptr, dc.ptr, T, M, K, stream.handle), "gemm")
     # the same product on split operands (int8 qs planes + fp32 scale planes)
@@ -1312,7 +1358,7 @@ def gemm_profile_pass(T: int = 512, M: int = 11008, K: int = 4096, copies: int =
         native.check(lib.asmhip_gemm_q8_split(q.ptr, sc.ptr, planes[2].ptr, planes[3].ptr, dc.ptr, T, M, K,
                                               stream.handle), "gemm split")
     stream.synchronize()
-    log(f"GEMM profile pass: {launches} launches of each layout ({T}x{M}x{K})")
+    log(f"GEMM profile pass: {launches} launches of each form ({T}x{M}x{K})")
 
 
 # rocprofv3 passes for the GEMM (each within one pass's limit of 8 SQ and 2 GRBM
@@ -1330,14 +1376,17 @@ def gemm_counters(T: int = 512, M: int = 11008, K: int = 4096, timeout_s: int = 
     matrix-core busy fraction, int8 ops counted by the hardware (MOPS_I8 x 512)
     against 2 T M K, VALU instructions per 32x32 output tile and block, the shader
     clock (GUI-active cycles per XCD over the dispatch's duration); for the
-    block-form kernel and, under "split_layout", the split-operand one."""
+    tile-layout kernel and, under "block_layout" and "split_layout", the GGUF-block
+    and split-operand ones."""
     res = _pmc_passes(GEMM_PASSES, ["--gemm-profile-pass"],
-                      {"gemm": lambda n: "gemm_q8_0" in n, "split": lambda n: "gemm_q8_split" in n}, timeout_s)
+                      {"gemm": lambda n: "gemm_q8_0_tiled" in n, "block": lambda n: "gemm_q8_0_coalesced" in n,
+                       "split": lambda n: "gemm_q8_split" in n}, timeout_s)
     if res is None:
         return None
     out = _gemm_derived(res["gemm"], T, M, K)
-    if "split" in res:
-        out["split_layout"] = _gemm_derived(res["split"], T, M, K)
+    for key, name in (("block", "block_layout"), ("split", "split_layout")):
+        if key in res:
+            out[name] = _gemm_derived(res[key], T, M, K)
     return out
 
 

@@ -180,6 +180,29 @@ ASMHIP_API int asmhip_matmul_swiglu(int qtype, const void* blocks, const float* 
  * applied to a batch; the reference itself has no GEMM. */
 ASMHIP_API int asmhip_gemm_q8_0(const void* w_blocks, const void* a_blocks, float* c, int64_t T, int64_t M,
                                 int64_t K, void* stream);
+/* The same GEMM on operands arranged once into GEMM tiles, so that each K step of a
+ * workgroup's tile is one contiguous run per operand (the kernel's LDS-direct loads
+ * land it as it lies).  The tile layout is a permutation of the Q8_0 blocks: rows in
+ * tiles of 128 (W) or 64 (A), tiles in order, within a tile the K steps of two
+ * blocks, within a step the tile's rows, 68 bytes each (the two blocks as they lie
+ * in the GGUF row); rows past the last pad the last tile.  K % 64 == 0.  Sizes:
+ * asmhip_gemm_q8_0_tiled_weight_bytes(M, K), asmhip_gemm_q8_0_tiled_activation_bytes(T, K)
+ * (0 for invalid shapes).  Build W once with asmhip_gemm_q8_0_tile_weights (padding
+ * rows zero); build A from fp32 rows with asmhip_quantize_q8_0_tiled (the
+ * asmhip_quantize Q8_0 blocks written in tile order; padding rows are not written and
+ * reach only outputs that are not stored) or from Q8_0 blocks with
+ * asmhip_gemm_q8_0_tile_activations.  Operands 16-byte aligned.  C is bitwise that of
+ * asmhip_gemm_q8_0 on the same blocks.  No counterpart in the reference (it has no
+ * GEMM). */
+ASMHIP_API int64_t asmhip_gemm_q8_0_tiled_weight_bytes(int64_t M, int64_t K);
+ASMHIP_API int64_t asmhip_gemm_q8_0_tiled_activation_bytes(int64_t T, int64_t K);
+ASMHIP_API int asmhip_gemm_q8_0_tile_weights(const void* w_blocks, void* w_tiled, int64_t M, int64_t K,
+                                             void* stream);
+ASMHIP_API int asmhip_gemm_q8_0_tile_activations(const void* a_blocks, void* a_tiled, int64_t T, int64_t K,
+                                                 void* stream);
+ASMHIP_API int asmhip_quantize_q8_0_tiled(const float* x, void* a_tiled, int64_t T, int64_t K, void* stream);
+ASMHIP_API int asmhip_gemm_q8_0_tiled(const void* w_tiled, const void* a_tiled, float* c, int64_t T, int64_t M,
+                                      int64_t K, void* stream);
 /* The same GEMM with W in the split layout of asm_matmul_q8 (matmul_q8_avx2.asm:51-194):
  * int8 qs planes [rows][K] (16-byte aligned) and fp32 scale planes [rows][K/32], for W (M rows)
  * and A (T rows).  The activations are int8 too: quantize the fp32 rows with

@@ -251,3 +251,87 @@ def test_gemm_split_rejects_bad_arguments(hip):
     assert hip.asmhip_gemm_q8_split(p, None, p, p, p, 4, 4, 32, None) == bad
     assert hip.asmhip_quantize_q8_split(p, p + 8, p, 4, 32, None) == bad
     assert hip.asmhip_quantize_q8_split(p, p, p, 4, 40, None) == bad
+
+
+# ---- GEMM tile layout: the same blocks arranged so a workgroup's K step is contiguous --------
+
+def tile_layout(blocks, R):
+    """The GEMM tile layout by reshaping: rows padded with zeros to a multiple of R,
+    then [tile][K step of two blocks][row of the tile][68 bytes]."""
+    rows, nb, _ = blocks.shape
+    padded = -(-rows // R) * R
+    b = np.zeros((padded, nb, 34), np.uint8)
+    b[:rows] = blocks
+    return np.ascontiguousarray(b.reshape(padded // R, R, nb // 2, 68).transpose(0, 2, 1, 3)).reshape(-1)
+
+
+def _tiled(hip, w_blocks, a_blocks):
+    M, T, K = w_blocks.shape[0], a_blocks.shape[0], w_blocks.shape[1] * 32
+    dwb, dab = DeviceBuffer.from_numpy(w_blocks), DeviceBuffer.from_numpy(a_blocks)
+    dw = DeviceBuffer(hip.asmhip_gemm_q8_0_tiled_weight_bytes(M, K))
+    da = DeviceBuffer(hip.asmhip_gemm_q8_0_tiled_activation_bytes(T, K))
+    assert hip.asmhip_gemm_q8_0_tile_weights(dwb.ptr, dw.ptr, M, K, None) == 0, hip.asmhip_last_error()
+    assert hip.asmhip_gemm_q8_0_tile_activations(dab.ptr, da.ptr, T, K, None) == 0, hip.asmhip_last_error()
+    dc = DeviceBuffer(T * M * 4)
+    rc = hip.asmhip_gemm_q8_0_tiled(dw.ptr, da.ptr, dc.ptr, T, M, K, None)
+    assert rc == 0, hip.asmhip_last_error()
+    synchronize()
+    return dc.download(np.float32, (T, M)), dw.download(np.uint8, dw.nbytes), da.download(np.uint8, da.nbytes)
+
+
+@pytest.mark.parametrize("T,M,K", [(512, 11008, 4096), (64, 128, 128), (1, 1, 64), (7, 33, 64), (100, 1000, 1024),
+                                   (65, 257, 192), (130, 300, 320)])
+def test_gemm_tiled_equals_block_gemm(hip, oracle, T, M, K):
+    """Same blocks in the tile layout: C bitwise equal to asmhip_gemm_q8_0's, which the
+    oracle bounds; the tiling kernels equal the reshape form of the layout, padding zero."""
+    w_blocks, a_blocks = _problem(T * 5 + M + K, T, M, K)
+    c, wt, at = _tiled(hip, w_blocks, a_blocks)
+    np.testing.assert_array_equal(wt, tile_layout(w_blocks, 128))
+    np.testing.assert_array_equal(at, tile_layout(a_blocks, 64))
+    np.testing.assert_array_equal(c, _gemm(hip, w_blocks, a_blocks))
+    if T * M <= 200_000:
+        _assert_close(c, oracle.gemm_q8_0(w_blocks, a_blocks, NT), w_blocks, a_blocks, oracle)
+
+
+def test_gemm_tiled_subnormal_and_extreme_scales(hip, oracle):
+    T, M, K = 64, 128, 512
+    w_blocks, a_blocks = _problem(13, T, M, K)
+    rng = np.random.default_rng(15)
+    sub = np.array([2.0 ** -24, 3 * 2.0 ** -20, 2.0 ** -15, 6.0e-5], np.float16).view(np.uint8).reshape(-1, 2)
+    big = np.array([60000.0, 1024.5, 0.5], np.float16).view(np.uint8).reshape(-1, 2)
+    for blocks, pool in ((w_blocks, sub), (a_blocks, np.concatenate([sub, big]))):
+        pick = rng.integers(0, len(pool), blocks.shape[:2])
+        mask = rng.random(blocks.shape[:2]) < 0.3
+        blocks[mask, 0:2] = pool[pick[mask]]
+    np.testing.assert_array_equal(_tiled(hip, w_blocks, a_blocks)[0], oracle.gemm_q8_0(w_blocks, a_blocks, NT))
+
+
+def test_quantize_tiled_equals_quantize_then_tile(hip):
+    T, K = 70, 256
+    x = np.random.default_rng(21).standard_normal((T, K)).astype(np.float32)
+    dx, db = DeviceBuffer.from_numpy(x), DeviceBuffer(gguf.q8_0_nbytes(T, K))
+    n = hip.asmhip_gemm_q8_0_tiled_activation_bytes(T, K)
+    dt = DeviceBuffer.from_numpy(np.full(n, 0xA5, np.uint8))
+    assert hip.asmhip_quantize(native.Q8_0, dx.ptr, db.ptr, T, K, None) == 0
+    assert hip.asmhip_quantize_q8_0_tiled(dx.ptr, dt.ptr, T, K, None) == 0, hip.asmhip_last_error()
+    synchronize()
+    blocks = db.download(np.uint8, (T, K // 32, 34))
+    got = dt.download(np.uint8, n).reshape(-1, K // 64, 64, 68)  # [tile][step][row][68]
+    want = tile_layout(blocks, 64).reshape(got.shape)
+    rows = np.arange(got.shape[0] * 64).reshape(-1, 64)          # global row of each tile row
+    live = rows < T
+    np.testing.assert_array_equal(got.transpose(0, 2, 1, 3)[live], want.transpose(0, 2, 1, 3)[live])
+    assert np.all(got.transpose(0, 2, 1, 3)[~live] == 0xA5)      # padding rows are not written
+
+
+def test_gemm_tiled_rejects_bad_arguments(hip):
+    d = DeviceBuffer(1 << 20)
+    p = d.ptr
+    bad = native.ERR_INVALID_ARGUMENT
+    assert hip.asmhip_gemm_q8_0_tiled(p, p, p, 4, 4, 96, None) == bad       # K % 64
+    assert hip.asmhip_gemm_q8_0_tiled(p, p, p, 0, 4, 64, None) == bad       # T = 0
+    assert hip.asmhip_gemm_q8_0_tiled(p + 4, p, p, 4, 4, 64, None) == bad   # not 16-byte aligned
+    assert hip.asmhip_gemm_q8_0_tiled(p, None, p, 4, 4, 64, None) == bad
+    assert hip.asmhip_gemm_q8_0_tile_weights(p, p, 4, 96, None) == bad
+    assert hip.asmhip_gemm_q8_0_tile_activations(p + 2, p, 4, 64, None) == bad
+    assert hip.asmhip_quantize_q8_0_tiled(p, p, 4, 32, None) == bad

@@ -91,3 +91,17 @@ def test_gate_up_interleave_round_trip():
     np.testing.assert_array_equal(u2, up)
     with pytest.raises(ValueError):
         interleave_gate_up(gate[:20], up[:20])
+
+
+def test_gemm_tiled_sizes():
+    """Tile-layout sizes: rows padded to 128 (weights) or 64 (activations), K/32 blocks
+    of 34 bytes a row; 0 for shapes the tiled GEMM does not take."""
+    lib = native.try_load_native_library()
+    assert lib is not None
+    assert lib.asmhip_gemm_q8_0_tiled_weight_bytes(11008, 4096) == 11008 * 128 * 34
+    assert lib.asmhip_gemm_q8_0_tiled_weight_bytes(1000, 64) == 1024 * 2 * 34
+    assert lib.asmhip_gemm_q8_0_tiled_activation_bytes(512, 4096) == 512 * 128 * 34
+    assert lib.asmhip_gemm_q8_0_tiled_activation_bytes(65, 128) == 128 * 4 * 34
+    for bad in ((0, 64), (4, 96), (4, 0), (-1, 64)):
+        assert lib.asmhip_gemm_q8_0_tiled_weight_bytes(*bad) == 0
+        assert lib.asmhip_gemm_q8_0_tiled_activation_bytes(*bad) == 0
