@@ -822,7 +822,7 @@ def bench_stamps(launches: int = 64, copies: int = 32) -> dict:
         b.close()
     log(f"stamps: plain {t_pl:.3f} us/launch, stamped {t_st:.3f}; span {span.mean():.3f}, gap {gap.mean():.3f}")
     return {"workload": f"Q4_0 matvec {M}x{K}, {launches} back-to-back launches from one graph, {copies} weight copies",
-            "kernel": "gguf_mfma_stream<0,1,16,1,1,0,false,16> (stamped instantiation)",
+            "kernel": "gguf_mfma_stream<0,1,16,1,1,0,false,16,false,true> (stamped instantiation)",
             "stamped_y_bitwise_equal_plain": same,
             "plain_us_per_launch": round(t_pl, 3), "stamped_us_per_launch": round(t_st, 3),
             "events_us_since_first_wave": events,
@@ -1212,7 +1212,7 @@ def _pmc_passes(passes, workload: list[str], kinds: dict, timeout_s: int = 150) 
     return {k: {"counters": vals[k], "us": float(np.mean(durs[k])), "dispatches": len(durs[k])} for k in kinds}
 
 
-HEADLINE_KERNEL = "gguf_mfma_stream<0, 1, 16, 1, 1, 0, false, 16>"
+HEADLINE_KERNEL = "gguf_mfma_stream<0, 1, 16, 1, 1, 0, false, 16, false, false>"
 
 
 def kernel_trace(steps: int = 20, timeout_s: int = 300) -> dict | None:
@@ -1517,7 +1517,7 @@ def main() -> None:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": round(traffic["bytes"]) if traffic else None,
             "traffic_detail": traffic,
-            "kernel": "gguf_mfma_stream<0,1,16,1,1> (int8 MFMA, GGUF Q4_0)",
+            "kernel": "gguf_mfma_stream<0,1,16,1,1,0,false,16,false,false> (int8 MFMA, GGUF Q4_0)",
             "kernel_us_mean": round(mv["kernel_us_mean"], 3),
             "event_bracket_us": round(mv["event_bracket_us"], 3),
             "fp32_valu_kernel_us_mean": round(mv["fp32_kernel_us_mean"], 3),

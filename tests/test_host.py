@@ -105,3 +105,19 @@ def test_gemm_tiled_sizes():
     for bad in ((0, 64), (4, 96), (4, 0), (-1, 64)):
         assert lib.asmhip_gemm_q8_0_tiled_weight_bytes(*bad) == 0
         assert lib.asmhip_gemm_q8_0_tiled_activation_bytes(*bad) == 0
+
+
+def test_bench_trace_filters_name_built_kernels():
+    """bench.py picks the headline matvec and the GEMM forms out of rocprofv3 traces by
+    kernel name: every name it filters on is an instantiation the library holds."""
+    import shutil
+    import subprocess
+
+    import bench
+
+    if shutil.which("nm") is None or not native.LIB_PATH.exists():
+        pytest.skip("nm or the built library missing")
+    names = subprocess.run(["nm", "-C", str(native.LIB_PATH)], capture_output=True, text=True, check=True).stdout
+    assert bench.HEADLINE_KERNEL + "(" in names
+    for fragment in ("gemm_q8_0_tiled<", "gemm_q8_0_coalesced<", "gemm_q8_split("):
+        assert fragment in names, fragment
