@@ -1368,6 +1368,8 @@ GEMM_PASSES = (
      "SQ_ACTIVE_INST_VALU", "SQ_WAVES", "SQ_INSTS_LDS", "GRBM_GUI_ACTIVE"),
     ("SQ_INSTS_VALU_CVT", "SQ_INSTS_VALU_FMA_F32", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAIT_INST_ANY",
      "SQ_WAVE_CYCLES", "SQ_INSTS_SALU", "SQ_INSTS_VALU_MFMA_MOPS_F16", "GRBM_GUI_ACTIVE"),
+    # the staging path: L1 -> L2 read requests (64-byte lines), L2 hits and misses, texture-address busy
+    ("TCP_TCC_READ_REQ_sum", "TCC_HIT_sum", "TCC_MISS_sum", "TA_TA_BUSY_sum", "GRBM_GUI_ACTIVE"),
 )
 
 
@@ -1384,13 +1386,13 @@ def gemm_counters(T: int = 512, M: int = 11008, K: int = 4096, timeout_s: int = 
     if res is None:
         return None
     out = _gemm_derived(res["gemm"], T, M, K)
-    for key, name in (("block", "block_layout"), ("split", "split_layout")):
+    for key, name, bb in (("block", "block_layout", 34), ("split", "split_layout", 36)):
         if key in res:
-            out[name] = _gemm_derived(res[key], T, M, K)
+            out[name] = _gemm_derived(res[key], T, M, K, bb)
     return out
 
 
-def _gemm_derived(r: dict, T: int, M: int, K: int) -> dict:
+def _gemm_derived(r: dict, T: int, M: int, K: int, block_bytes: int = 34) -> dict:
     from asmllm_amd.device import device_info
 
     v, us = r["counters"], r["us"]
@@ -1417,7 +1419,20 @@ def _gemm_derived(r: dict, T: int, M: int, K: int) -> dict:
         "lds_insts_per_block_tile": round(v["SQ_INSTS_LDS"] / block_tiles, 2),
         "valu_issue_frac": round(4 * v["SQ_INSTS_VALU"] / (gui * simds), 4),
         "lds_bank_conflict_frac_of_lds_active": round(v["SQ_LDS_BANK_CONFLICT"] / max(v["SQ_LDS_IDX_ACTIVE"], 1), 4),
+        "l2_read_requests": round(v["TCP_TCC_READ_REQ_sum"], 0),
+        "l2_read_requests_per_64_staged_bytes": round(
+            64 * v["TCP_TCC_READ_REQ_sum"] / _gemm_staged_bytes(T, M, K, block_bytes), 3),
+        "l2_hit_rate": round(v["TCC_HIT_sum"] / max(v["TCC_HIT_sum"] + v["TCC_MISS_sum"], 1), 4),
+        "ta_busy_frac": round(v["TA_TA_BUSY_sum"] / (cus * gui), 4),
     }
+
+
+def _gemm_staged_bytes(T: int, M: int, K: int, block_bytes: int = 34, tt: int = 64, tm: int = 128) -> int:
+    """Operand bytes the 64 x 128 workgroup tiles stage from L2 in all: every
+    tile reads its 64 A rows and 128 W rows over the whole of K (block_bytes a
+    block: 34 in GGUF blocks, 36 as split int8 qs + an fp32 scale)."""
+    tiles = -(-T // tt) * -(-M // tm)
+    return tiles * (tt + tm) * (K // 32) * block_bytes
 
 
 def main() -> None:
