@@ -973,9 +973,7 @@ def bench_gemm(T: int = 512, M: int = 11008, K: int = 4096, copies: int = 12) ->
         native.check(lib.asmhip_quantize(native.Q8_0, da.ptr, dq.ptr, T, K, st), "quantize")
 
     us = time_launches(gemm_tiled, copies, reps=20)
-    us_qt = time_launches(quant_tiled, copies, reps=20)
-    # restore the random activation blocks the other forms use
-    native.check(lib.asmhip_gemm_q8_0_tile_activations(dq.ptr, dqt.ptr, T, K, None), "tile activations")
+    us_qt = time_launches(quant_tiled, copies, reps=20)  # (overwrites dqt; the block form reads dq)
     us_b = time_launches(gemm, copies, reps=20)
     us_q = time_launches(quant, copies, reps=20)
     ops = 2 * T * M * K
