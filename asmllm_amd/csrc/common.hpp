@@ -86,6 +86,24 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// DPP controls: quad_perm [1,0,3,2] and [2,3,0,1] (lanes ^1 and ^2 within a
+// quad), row_half_mirror, row_mirror.
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppRowHalfMirror = 0x141, kDppRowMirror = 0x140;
+
+// Sum over the 64 lanes of a wave without LDS: each 16-lane row is summed
+// with DPP adds (every lane of a row gets its row's sum), then the four row
+// sums are added in row order, ((r0 + r1) + r2) + r3, a wave-uniform value.
+__device__ __forceinline__ float wave_total_dpp(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppQuadXor1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppQuadXor2, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppRowHalfMirror, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppRowMirror, 0xF, 0xF, false));
+    const int b = __float_as_int(v);
+    return ((__int_as_float(__builtin_amdgcn_readlane(b, 0)) + __int_as_float(__builtin_amdgcn_readlane(b, 16))) +
+            __int_as_float(__builtin_amdgcn_readlane(b, 32))) +
+           __int_as_float(__builtin_amdgcn_readlane(b, 48));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

@@ -590,7 +590,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
                     ss = fmaf(xv[i][h].w, xv[i][h].w, ss);
                 }
             }
-        ss = wave_sum(ss);
+        ss = wave_total_dpp(ss);
         if (lane == 0) red[wave] = ss;
 #pragma unroll
         for (int i = 0; i < XQ; ++i)
@@ -627,8 +627,9 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         uint32_t mb = 0u;
 #pragma unroll
         for (int t = 0; t < 8; ++t) mb = max(mb, __float_as_uint(v[t]) & 0x7FFFFFFFu);
-        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1, 64));
-        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 2, 64));
+        // quad max through DPP (lanes ^1, ^2): no LDS round trip on the way to the digits
+        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, kDppQuadXor1, 0xF, 0xF, false));
+        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, kDppQuadXor2, 0xF, 0xF, false));
         const bool finite = mb < 0x7F800000u;
         const float mx = __uint_as_float(finite ? mb : 0u);
         int e;
@@ -667,6 +668,16 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     }
     __syncthreads();
     mark(2);
+    // RMSNorm: every wave's sum of squares is in red[] once x's digits are
+    // (the barrier above), so the scale is formed now, while the first units
+    // are in flight, instead of after the stream
+    float inv = 1.f;
+    if (!AM && pre == kPreRmsNorm) {
+        float tot = 0.f;
+#pragma unroll
+        for (int k = 0; k < NW; ++k) tot += red[k];
+        inv = 1.0f / sqrtf(tot / (float)K + eps);
+    }
 
     // 4) the stream: stage unit s, multiply, refill its buffer with unit s + D.
     constexpr int kPairs = kUnitBlocks / 2;
@@ -750,13 +761,6 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
 
     // 5) add the waves' partial sums of every row in a fixed order (RMSNorm:
     // then scale the total by inv).
-    float inv = 1.f;
-    if (!AM && pre == kPreRmsNorm) {
-        float tot = 0.f;
-#pragma unroll
-        for (int k = 0; k < NW; ++k) tot += red[k];
-        inv = 1.0f / sqrtf(tot / (float)K + eps);
-    }
     if (post == kPostSwiGlu8) {
         // a tile is 8 gate rows and their 8 up rows (M % 16 == 0, TH = 16): y[8 tile + r] = silu(gate) * up
         for (int idx = threadIdx.x; idx < my_tiles * 8; idx += kThreads) {
