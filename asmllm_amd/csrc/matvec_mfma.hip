@@ -555,7 +555,10 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     }
 
     // 3) fused pre-op on x, then digits; partial sums start at zero.
-    for (int i = threadIdx.x; i < my_tiles * NW * 16; i += kThreads) part[i] = 0.f;
+    // partial sums start at zero where some wave streams no unit of a tile
+    // (fewer units per tile than waves); otherwise every entry is written
+    if (nu < NW)
+        for (int i = threadIdx.x; i < my_tiles * NW * 16; i += kThreads) part[i] = 0.f;
     if constexpr (AM) {
         if (am_items && pre_hd == 128) {
             // branch-free pick of head lane >> 4 of the four: bitwise selects on the
@@ -616,7 +619,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     for (int i = 0; i < XQ; ++i) {
         // a wave whose items of this round are all past the last one skips the
         // round (wave-uniform), leaving its SIMD to the waves that have items
-        if (i > 0 && kThreads * i + 64 * wave >= ni) break;
+        if (kThreads * i + 64 * wave >= ni) break;
         const int it = (int)threadIdx.x + kThreads * i;
         const float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
                             xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
