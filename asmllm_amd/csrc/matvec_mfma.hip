@@ -372,7 +372,7 @@ __device__ __forceinline__ float tile_total(float acc) {
 // ST (measurement only): every wave records the 100 MHz real-time counter at
 // kStampCount points of its life into stamps[(block * NW + wave) * kStampCount + i].
 constexpr int kStampCount = 8;
-template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH, bool RP, bool ST = false>
+template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH, bool RP, bool ST = false, bool XW = false>
 __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __restrict__ w,
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ pre_arg,
@@ -491,6 +491,18 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         } else if (am_items) {
             am.load(ph, pre_hd + 4, off - hh * pre_hd);
         }
+    } else if constexpr (XW) {
+        static_assert(PW == 0 && AMS == 0, "x per wave: the any-K stream without a merge");
+        // only the items of this wave's own units (the same units in every tile):
+        // round i holds units 2i (lanes 0-31) and 2i + 1 (lanes 32-63) of the wave
+#pragma unroll
+        for (int i = 0; i < XQ; ++i) {
+            const int j = 2 * i + (lane >> 5);
+            const int it = (j < per_w ? wave + NW * j : wave) * 32 + (lane & 31);
+            const int off = 32 * (it >> 2) + 4 * (it & 3);
+            xv[i][0] = *reinterpret_cast<const float4*>(x + off);
+            xv[i][1] = *reinterpret_cast<const float4*>(x + off + 16);
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < XQ; ++i) {
@@ -576,6 +588,8 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         }
         if (am_items) am.finish(&xv[0][0], &xv[0][1]);
         else xv[0][0] = xv[0][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // no item: no digit writes below
+    } else if (XW) {
+        // no pre-op (the host launches XW only without one)
     } else if (pre == kPreRmsNorm) {
         // RMSNorm without a barrier before the digits: y = W (inv (x * g)) =
         // inv (W (x * g)), so x * g is digitized now and every row total is
@@ -619,8 +633,9 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     for (int i = 0; i < XQ; ++i) {
         // a wave whose items of this round are all past the last one skips the
         // round (wave-uniform), leaving its SIMD to the waves that have items
-        if (kThreads * i + 64 * wave >= ni) break;
-        const int it = (int)threadIdx.x + kThreads * i;
+        if (XW ? 2 * i >= per_w : kThreads * i + 64 * wave >= ni) break;
+        const int jw = 2 * i + (lane >> 5);  // XW: this lane's unit of the wave
+        const int it = XW ? (jw < per_w ? wave + NW * jw : wave) * 32 + (lane & 31) : (int)threadIdx.x + kThreads * i;
         const float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
                             xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
         // the 4 items of a block sit in 4 consecutive lanes.  The block maximum
@@ -652,7 +667,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         transpose_digits(Y1 + 4, d1h);
         transpose_digits(Y2, d2l);
         transpose_digits(Y2 + 4, d2h);
-        if (it < ni) {
+        if (XW ? jw < per_w : it < ni) {
             // digit row r (0-3 X1, 4-7 X2, top digit first) of half hh = g / 2 of block b:
             // 16 bytes at hh * 128 + 16 r; positions 4g..4g+3 go to bytes 4 (g & 1) ..,
             // positions 16+4g..16+4g+3 to bytes 8 + 4 (g & 1) ..
@@ -669,7 +684,13 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
                 xscale[b] = finite ? ldexpf(1.0f, e - Fmt<QT>::kXScaleShift) : __builtin_nanf("");
         }
     }
-    __syncthreads();
+    // XW: a wave reads only the digits it wrote (its own units' blocks), and
+    // LDS operations of one wave complete in order: no workgroup barrier, each
+    // wave starts its stream as soon as its own digits are in
+    if constexpr (XW)
+        __builtin_amdgcn_wave_barrier();
+    else
+        __syncthreads();
     mark(2);
     // RMSNorm: every wave's sum of squares is in red[] once x's digits are
     // (the barrier above), so the scale is formed now, while the first units
@@ -818,13 +839,14 @@ struct Planes {
     const float* wsc;
 };
 
-template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH, bool RP>
+template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH, bool RP, bool XW = false>
 int launch_rp(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
-    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH, RP>;
+    const void* fn = (const void*)gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH, RP, false, XW>;
     const int rc = dynamic_lds(fn, lds);
     if (rc) return rc;
-    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH, RP>), dim3(grid), dim3(NW * 64), lds, st,
+    hipLaunchKernelGGL((gguf_mfma_stream<QT, XQ, NW, D, PW, AMS, NTW, TH, RP, false, XW>), dim3(grid), dim3(NW * 64),
+                       lds, st,
                        pw.w, x, o.pre_arg, pw.wh, pw.wsc, M, K, o.pre, y, o.eps, (int)o.accumulate, o.post,
                        o.attn_hd, nullptr);
     return kOk;
@@ -843,11 +865,31 @@ int launch_xq(const Planes& pw, const float* x, float* y, int M, int K, int grid
     return launch_rp<QT, XQ, NW, D, PW, AMS, NTW, TH, false>(pw, x, y, M, K, grid, lds, st, o);
 }
 
+// Q4_0, any K other than 4096 at 16 waves, no pre-op, every wave with a unit of
+// every tile: each wave digitizes only its own units' x (XW), with no
+// workgroup barrier before the stream.  Rounds of two units per wave.
+template <int NW, int D>
+int launch_xw(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
+              const MatvecOpts& o) {
+    const int nu = K / 32 / kUnitBlocks;
+    const int rounds = ((nu + NW - 1) / NW + 1) / 2;
+    if (o.accumulate)
+        return rounds <= 1 ? launch_rp<kFmtQ4_0, 1, NW, D, 0, 0, false, 16, true, true>(pw, x, y, M, K, grid, lds, st, o)
+                           : launch_rp<kFmtQ4_0, 2, NW, D, 0, 0, false, 16, true, true>(pw, x, y, M, K, grid, lds, st, o);
+    return rounds <= 1 ? launch_rp<kFmtQ4_0, 1, NW, D, 0, 0, false, 16, false, true>(pw, x, y, M, K, grid, lds, st, o)
+                       : launch_rp<kFmtQ4_0, 2, NW, D, 0, 0, false, 16, false, true>(pw, x, y, M, K, grid, lds, st, o);
+}
+
 // x items (8 positions) per thread -> the matching instantiation
 template <int QT, int NW, int D>
 int launch_nw(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
     const int nb = K / 32;
+    if constexpr (QT == kFmtQ4_0 && NW == kWideWaves) {
+        const int nu = nb / kUnitBlocks;
+        if (o.pre == kPreNone && o.post == kPostNone && nu >= NW && (nu + NW - 1) / NW <= 4)
+            return launch_xw<NW, D>(pw, x, y, M, K, grid, lds, st, o);
+    }
     const int xq = (nb * 4 + NW * 64 - 1) / (NW * 64);
     if (xq <= 1) return launch_xq<QT, 1, NW, D, 0>(pw, x, y, M, K, grid, lds, st, o);
     if constexpr (NW >= 16) {  // nb <= 512: at most 2 items per thread
