@@ -492,7 +492,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
             am.load(ph, pre_hd + 4, off - hh * pre_hd);
         }
     } else if constexpr (XW) {
-        static_assert(PW == 0 && AMS == 0, "x per wave: the any-K stream without a merge");
+        static_assert(AMS == 0 && PW == 0, "x per wave: the any-K stream, no merge");
         // only the items of this wave's own units (the same units in every tile):
         // round i holds units 2i (lanes 0-31) and 2i + 1 (lanes 32-63) of the wave
 #pragma unroll
@@ -502,6 +502,10 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
             const int off = 32 * (it >> 2) + 4 * (it & 3);
             xv[i][0] = *reinterpret_cast<const float4*>(x + off);
             xv[i][1] = *reinterpret_cast<const float4*>(x + off + 16);
+            if (pre != kPreNone) {
+                av[i][0] = *reinterpret_cast<const float4*>(pre_arg + off);
+                av[i][1] = *reinterpret_cast<const float4*>(pre_arg + off + 16);
+            }
         }
     } else {
 #pragma unroll
@@ -588,17 +592,15 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
         }
         if (am_items) am.finish(&xv[0][0], &xv[0][1]);
         else xv[0][0] = xv[0][1] = make_float4(0.f, 0.f, 0.f, 0.f);  // no item: no digit writes below
-    } else if (XW) {
-        // no pre-op (the host launches XW only without one)
     } else if (pre == kPreRmsNorm) {
         // RMSNorm without a barrier before the digits: y = W (inv (x * g)) =
         // inv (W (x * g)), so x * g is digitized now and every row total is
-        // scaled by inv = 1 / sqrt(mean(x^2) + eps) after the stream, from the
-        // waves' sums of squares (read after the barrier that ends the stream)
+        // scaled by inv = 1 / sqrt(mean(x^2) + eps) from the waves' sums of
+        // squares (XW: the waves' units cover every block of x exactly once)
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < XQ; ++i)
-            if ((int)threadIdx.x + kThreads * i < ni) {
+            if (XW ? 2 * i + (lane >> 5) < per_w : (int)threadIdx.x + kThreads * i < ni) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     ss = fmaf(xv[i][h].x, xv[i][h].x, ss);
@@ -694,14 +696,16 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     mark(2);
     // RMSNorm: every wave's sum of squares is in red[] once x's digits are
     // (the barrier above), so the scale is formed now, while the first units
-    // are in flight, instead of after the stream
+    // are in flight, instead of after the stream (XW, with no barrier here:
+    // after the barrier that ends the stream)
     float inv = 1.f;
-    if (!AM && pre == kPreRmsNorm) {
+    auto rms_scale = [&]() {
         float tot = 0.f;
 #pragma unroll
         for (int k = 0; k < NW; ++k) tot += red[k];
-        inv = 1.0f / sqrtf(tot / (float)K + eps);
-    }
+        return 1.0f / sqrtf(tot / (float)K + eps);
+    };
+    if (!XW && !AM && pre == kPreRmsNorm) inv = rms_scale();
 
     // 4) the stream: stage unit s, multiply, refill its buffer with unit s + D.
     constexpr int kPairs = kUnitBlocks / 2;
@@ -782,6 +786,7 @@ __global__ __launch_bounds__(NW * 64) void gguf_mfma_stream(const uint8_t* __res
     mark(5);
     __syncthreads();
     mark(6);
+    if (XW && pre == kPreRmsNorm) inv = rms_scale();  // XW: red[] is complete only here
 
     // 5) add the waves' partial sums of every row in a fixed order (RMSNorm:
     // then scale the total by inv).
@@ -887,7 +892,7 @@ int launch_nw(const Planes& pw, const float* x, float* y, int M, int K, int grid
     const int nb = K / 32;
     if constexpr (QT == kFmtQ4_0 && NW == kWideWaves) {
         const int nu = nb / kUnitBlocks;
-        if (o.pre == kPreNone && o.post == kPostNone && nu >= NW && (nu + NW - 1) / NW <= 4)
+        if ((o.pre == kPreNone || o.pre == kPreRmsNorm) && o.post == kPostNone && nu >= NW && (nu + NW - 1) / NW <= 4)
             return launch_xw<NW, D>(pw, x, y, M, K, grid, lds, st, o);
     }
     const int xq = (nb * 4 + NW * 64 - 1) / (NW * 64);

@@ -464,10 +464,15 @@ def _fused(hip, qtype, blocks, x, pre, arg, eps, y0):
 @pytest.mark.parametrize("qt,kernel", [("q4", native.Q4_KERNEL_FP32), ("q4", native.Q4_KERNEL_MFMA),
                                        ("q8", native.Q4_KERNEL_AUTO), ("q8", native.Q4_KERNEL_FP32)],
                          ids=["q4-fp32", "q4-mfma", "q8", "q8-fp32"])
-@pytest.mark.parametrize("pre", ["none", "rmsnorm", "swiglu"])
+@pytest.mark.parametrize("pre", ["none", "rmsnorm", "swiglu", "rmsnorm-k11008", "none-k11008"])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_fused_matvec(hip, oracle, q4_kernel, qt, kernel, pre, accumulate):
-    M, K = 1000, 4096 if pre != "swiglu" else 11008
+    """The matvec with its pre-op fused into the read of x, overwriting or
+    accumulating.  K = 11008 takes the stream where each wave digitizes only its
+    own units' x (Q4_0 MFMA; with RMSNorm the waves' sums of squares meet after
+    the stream)."""
+    pre, _, kk = pre.partition("-k")
+    M, K = 1000, int(kk) if kk else 4096 if pre != "swiglu" else 11008
     q4_kernel(kernel)
     blocks, x = _weights(17 + K, M, K, qt)
     rng = np.random.default_rng(5)
