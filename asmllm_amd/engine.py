@@ -324,6 +324,12 @@ class DecodeEngine:
     def enqueue_step(self) -> None:
         """Launches one token step on the engine's stream: logits for the token
         in ``token`` at position ``pos``, then token <- argmax, pos += 1."""
+        for _kind, _layer, launch in self.step_launches():
+            launch()
+
+    def step_launches(self):
+        """The launches of one token step in order, as (kind, layer or None,
+        launch): kinds embed, qkv, attention, o, gate_up, down, lm_head, argmax."""
         s, L, st = self.shape, self.lib, self.stream.handle
         d, h, hd = s.dim, s.hidden_dim, s.head_dim
         eps = ctypes.c_float(s.eps)
@@ -342,23 +348,34 @@ class DecodeEngine:
             xin, pre, arg = norm_in(norm)
             mv(w, xin, y, M, d, pre, arg, 0, what, qtype)
 
-        embed = L.asmhip_embed_q8_0 if self.embed_type == native.Q8_0 else L.asmhip_embed_q4_0
-        check(embed(self.embed.ptr, self.token.ptr, self.x.ptr, s.vocab, d, st), "embed")
-        for ly in self.layers:
-            normed(ly.attn_norm, s.qkv_rows, ly.wqkv, self.qkv.ptr, "qkv matvec")
+        def attention(ly):
             check(L.asmhip_attention_decode_partials_rope_table(self.qkv.ptr, ly.k_cache.ptr, ly.v_cache.ptr,
                                                                 self.workspace.ptr, s.n_heads, s.n_kv_heads, hd,
                                                                 self.pos.ptr, self.max_ctx, self.rope_table.ptr, st),
                   "rope + attention")
-            check(L.asmhip_matmul_attn_output(Q4, ly.wo.ptr, self.workspace.ptr, self.attn.ptr, self.x.ptr, d,
-                                              s.n_heads, hd, self.max_ctx, 1, st), "merge + o matvec")
+
+        def gate_up(ly):
             xin, pre, arg = norm_in(ly.ffn_norm)
             check(L.asmhip_matmul_swiglu(Q4, ly.wgu.ptr, xin, self.ffn.ptr, h, d, pre, arg, eps, self.gu.ptr, st),
                   "gate/up matvec + swiglu")
-            mv(ly.wdown, self.ffn.ptr, self.x.ptr, d, h, NONE, None, 1, "down matvec")
-        normed(self.final_norm, s.vocab, self.output, self.logits.ptr, "lm-head matvec", self.output_type)
-        check(L.asmhip_argmax_history(self.logits.ptr, s.vocab, self.token.ptr, self.pos.ptr, self.history.ptr,
-                                      self.max_ctx, st), "argmax")
+
+        embed = L.asmhip_embed_q8_0 if self.embed_type == native.Q8_0 else L.asmhip_embed_q4_0
+        yield "embed", None, lambda: check(embed(self.embed.ptr, self.token.ptr, self.x.ptr, s.vocab, d, st),
+                                           "embed")
+        for i, ly in enumerate(self.layers):
+            yield "qkv", i, lambda ly=ly: normed(ly.attn_norm, s.qkv_rows, ly.wqkv, self.qkv.ptr, "qkv matvec")
+            yield "attention", i, lambda ly=ly: attention(ly)
+            yield "o", i, lambda ly=ly: check(L.asmhip_matmul_attn_output(Q4, ly.wo.ptr, self.workspace.ptr,
+                                                                           self.attn.ptr, self.x.ptr, d, s.n_heads,
+                                                                           hd, self.max_ctx, 1, st),
+                                               "merge + o matvec")
+            yield "gate_up", i, lambda ly=ly: gate_up(ly)
+            yield "down", i, lambda ly=ly: mv(ly.wdown, self.ffn.ptr, self.x.ptr, d, h, NONE, None, 1, "down matvec")
+        yield "lm_head", None, lambda: normed(self.final_norm, s.vocab, self.output, self.logits.ptr,
+                                              "lm-head matvec", self.output_type)
+        yield "argmax", None, lambda: check(L.asmhip_argmax_history(self.logits.ptr, s.vocab, self.token.ptr,
+                                                                    self.pos.ptr, self.history.ptr, self.max_ctx,
+                                                                    st), "argmax")
 
     def set_position(self, token_id: int, pos: int) -> None:
         if not 0 <= pos < self.max_ctx:

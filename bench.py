@@ -1117,6 +1117,71 @@ def bench_decode(steps: int = 128, context: int = 2048, warmup: int = 4, eager: 
             "cpu_baseline": cpu}
 
 
+def bench_decode_launches(context: int = 2048, reps: int = 8, per_graph: int = 256) -> dict:
+    """Each launch kind of the 7B decode step timed on its own, back to back in
+    graph replay, in the state of a real token step at position `context`: one
+    whole step runs first (every buffer then holds that step's values), then
+    the launches of one kind (qkv, attention, o, gate_up, down over the 32
+    layers' own weights and caches; lm_head, embed, argmax once a step) are
+    captured `per_graph` launches to a graph and replayed `reps` times.  The
+    attention reads positions 0..context of the layer's cache; argmax runs last
+    (it advances the position).  bytes: what the launch reads from HBM."""
+    from asmllm_amd.device import Event, Graph, synchronize
+    from asmllm_amd.engine import LLAMA_7B, DecodeEngine
+    from asmllm_amd.gguf import q4_0_nbytes
+
+    s = LLAMA_7B
+    d, h, hd = s.dim, s.hidden_dim, s.head_dim
+    eng = DecodeEngine(s, max_ctx=context + 128)
+    eng.init_random(seed=42)
+    eng.set_position(1, context)
+    eng.enqueue_step()
+    eng.stream.synchronize()
+    launches = list(eng.step_launches())
+    kv = s.n_kv_heads * (context + 1) * hd * 2 * 2  # k and v rows 0..context of one layer, fp16
+    nbytes = {
+        "qkv": q4_0_nbytes(s.qkv_rows, d) + 4 * d, "attention": kv,
+        "o": q4_0_nbytes(d, d) + 4 * s.n_heads * attn_splits_of(context + 128) * (hd + 4),
+        "gate_up": q4_0_nbytes(2 * h, d) + 4 * d, "down": q4_0_nbytes(d, h) + 4 * h,
+        "lm_head": q4_0_nbytes(s.vocab, d) + 4 * d, "embed": (d // 32) * 18, "argmax": 4 * s.vocab,
+    }
+    out = {}
+    for kind in ("qkv", "attention", "o", "gate_up", "down", "lm_head", "embed", "argmax"):
+        eng.set_position(1, context)
+        fns = [f for k, _, f in launches if k == kind]
+        rounds = max(1, per_graph // len(fns))
+        graph = Graph.capture(eng.stream, lambda: [f() for _ in range(rounds) for f in fns])
+        graph.launch(eng.stream)
+        eng.stream.synchronize()
+        if kind == "argmax":
+            eng.set_position(1, context)
+        synchronize()
+        e0, e1 = Event(timing=True), Event(timing=True)
+        e0.record(eng.stream)
+        for _ in range(reps):
+            graph.launch(eng.stream)
+        e1.record(eng.stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / (reps * rounds * len(fns))
+        graph.close()
+        out[kind] = {"us": round(us, 3), "per_token": len(fns), "bytes": int(nbytes[kind]),
+                     "GBps": round(nbytes[kind] / (us * 1e-6) / 1e9, 1)}
+    eng.close()
+    layer = sum(out[k]["us"] for k in ("qkv", "attention", "o", "gate_up", "down"))
+    token = sum(v["us"] * v["per_token"] for v in out.values())
+    log(f"decode launches: layer {layer:.2f} us, token {token:.1f} us (sum of the launches, one kind at a time)")
+    return {"workload": f"7B-shape Q4_0 decode step at position {context}, each launch kind back to back in "
+                        f"graphs of {per_graph}; lm_head / embed / argmax repeat the one launch of a step "
+                        "(its weights then stay in the MALL)",
+            "launches": out, "layer_us": round(layer, 2), "token_us_sum": round(token, 1)}
+
+
+def attn_splits_of(max_ctx: int) -> int:
+    """Splits of the decode attention at this cache length (384 positions up to 3072, else 512)."""
+    sl = 384 if max_ctx <= 3072 else 512
+    return -(-max_ctx // sl)
+
+
 def profile_pass(copies: int, launches: int = 64) -> None:
     """A short fixed workload for hardware-counter runs: `launches` matvecs over
     rotating weight copies, then the calibration kernel (exact Q4_0 dequantization
@@ -1449,7 +1514,7 @@ def main() -> None:
     ap.add_argument("--no-trace", action="store_true", help="skip the rocprofv3 kernel trace of the timed region")
     ap.add_argument("--no-extra", action="store_true", help="skip the shape table, GEMM and decode legs")
     ap.add_argument("--only", choices=["decode", "gemm", "table", "floor", "host", "cpu", "traffic", "gemm_counters",
-                                       "phases", "trace", "stamps"],
+                                       "phases", "trace", "stamps", "decode_launches"],
                     help="run one extra leg and print its JSON")
     ap.add_argument("--eager", action="store_true", help="with --only: launch without graphs")
     args = ap.parse_args()
@@ -1478,7 +1543,8 @@ def main() -> None:
             res = {"gemm": bench_gemm, "table": bench_matvec_table, "floor": bench_read_floor,
                    "host": bench_host_pointer, "traffic": measure_traffic,
                    "gemm_counters": gemm_counters, "phases": bench_matvec_phases,
-                   "trace": kernel_trace, "stamps": bench_stamps}[args.only]()
+                   "trace": kernel_trace, "stamps": bench_stamps,
+                   "decode_launches": bench_decode_launches}[args.only]()
         print(json.dumps({args.only: res}), flush=True)
         return
 
