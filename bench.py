@@ -1275,7 +1275,7 @@ def _pmc_passes(passes, workload: list[str], kinds: dict, timeout_s: int = 150) 
     return {k: {"counters": vals[k], "us": float(np.mean(durs[k])), "dispatches": len(durs[k])} for k in kinds}
 
 
-HEADLINE_KERNEL = "gguf_mfma_stream<0, 1, 16, 1, 1, 0, false, 16, false, false, false>"
+HEADLINE_KERNEL = "gguf_mfma_stream<0, 1, 16, 1, 1, 0, false, 16, false, false, false, false>"
 
 
 def kernel_trace(steps: int = 20, timeout_s: int = 300) -> dict | None:
@@ -1596,7 +1596,7 @@ def main() -> None:
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": round(traffic["bytes"]) if traffic else None,
             "traffic_detail": traffic,
-            "kernel": "gguf_mfma_stream<0,1,16,1,1,0,false,16,false,false,false> (int8 MFMA, GGUF Q4_0)",
+            "kernel": "gguf_mfma_stream<0,1,16,1,1,0,false,16,false,false,false,false> (int8 MFMA, GGUF Q4_0)",
             "kernel_us_mean": round(mv["kernel_us_mean"], 3),
             "event_bracket_us": round(mv["event_bracket_us"], 3),
             "fp32_valu_kernel_us_mean": round(mv["fp32_kernel_us_mean"], 3),
