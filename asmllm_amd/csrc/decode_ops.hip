@@ -560,29 +560,47 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
             }
         }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(v, o, kWave);
-        const int oi = __shfl_xor(idx, o, kWave);
+    // the (value, index) order is total, so any reduction order gives the same
+    // winner: within each 16-lane row through DPP, then the four rows of a wave
+    // and the 16 waves in order (no LDS round trips inside a wave)
+    auto take = [&](float ov, int oi) {
         if (argmax_better(ov, oi, v, idx)) {
             v = ov;
             idx = oi;
         }
-    }
+    };
+    auto row_reduce = [&]() {
+        take(__int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppQuadXor1, 0xF, 0xF, false)),
+             __builtin_amdgcn_update_dpp(0, idx, kDppQuadXor1, 0xF, 0xF, false));
+        take(__int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppQuadXor2, 0xF, 0xF, false)),
+             __builtin_amdgcn_update_dpp(0, idx, kDppQuadXor2, 0xF, 0xF, false));
+        take(__int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppRowHalfMirror, 0xF, 0xF, false)),
+             __builtin_amdgcn_update_dpp(0, idx, kDppRowHalfMirror, 0xF, 0xF, false));
+        take(__int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kDppRowMirror, 0xF, 0xF, false)),
+             __builtin_amdgcn_update_dpp(0, idx, kDppRowMirror, 0xF, 0xF, false));
+    };
+    row_reduce();  // every lane holds its row's winner
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    {
+        const int vb = __float_as_int(v), ib = idx;
+        v = __int_as_float(__builtin_amdgcn_readlane(vb, 0));
+        idx = __builtin_amdgcn_readlane(ib, 0);
+#pragma unroll
+        for (int r = 1; r < 4; ++r)
+            take(__int_as_float(__builtin_amdgcn_readlane(vb, 16 * r)), __builtin_amdgcn_readlane(ib, 16 * r));
+    }
     if (lane == 0) {
         bv[w] = v;
         bi[w] = idx;
     }
     __syncthreads();
+    if (w == 0) {
+        v = lane < 16 ? bv[lane] : -INFINITY;
+        idx = lane < 16 ? bi[lane] : 0x7fffffff;
+        row_reduce();  // lanes 0-15 hold the winner of the 16 waves
+    }
     if (threadIdx.x == 0) {
-        float best = bv[0];
-        int bidx = bi[0];
-        for (int i = 1; i < 16; ++i)
-            if (argmax_better(bv[i], bi[i], best, bidx)) {
-                best = bv[i];
-                bidx = bi[i];
-            }
+        const int bidx = idx;
         *token = bidx;
         if (pos) {
             // history[p] = the token chosen at position p, so that a graph of
