@@ -211,10 +211,12 @@ def bench_matvec(steps: int, warmup: int, copies: int) -> dict:
             g.close()
         return ms, wall
 
-    total_ms, wall_s = timed(steps)
     # the same bracketing with no launch between the events: what recording the two
-    # events adds to the region (~3-4 us: a few percent of 20 steps, nothing at 4096)
+    # events adds to the region (~3-4 us: a few percent of 20 steps, nothing at 4096);
+    # taken first, so that the timed launches are the last headline dispatches of a
+    # run (the kernel-trace leg reads them from the end of the trace)
     bracket_ms = min(timed(0)[0] for _ in range(3))
+    total_ms, wall_s = timed(steps)
     bytes_step = q4_algorithmic_bytes(M, K)
     selected = lib.asmhip_get_q4_kernel()
     # the fp32 VALU kernel on the same copies, for reference
@@ -822,7 +824,7 @@ def bench_stamps(launches: int = 64, copies: int = 32) -> dict:
         b.close()
     log(f"stamps: plain {t_pl:.3f} us/launch, stamped {t_st:.3f}; span {span.mean():.3f}, gap {gap.mean():.3f}")
     return {"workload": f"Q4_0 matvec {M}x{K}, {launches} back-to-back launches from one graph, {copies} weight copies",
-            "kernel": "gguf_mfma_stream<0,1,16,1,1,0,false,16,false,true> (stamped instantiation)",
+            "kernel": "gguf_mfma_stream<0,1,16,1,1,0,false,16,false,true,false,false> (stamped instantiation)",
             "stamped_y_bitwise_equal_plain": same,
             "plain_us_per_launch": round(t_pl, 3), "stamped_us_per_launch": round(t_st, 3),
             "events_us_since_first_wave": events,
