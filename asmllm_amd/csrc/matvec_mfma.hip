@@ -371,6 +371,12 @@ __device__ __forceinline__ float tile_total(float acc) {
 // one would cost a kernel-argument load in front of the weight stream).
 // ST (measurement only): every wave records the 100 MHz real-time counter at
 // kStampCount points of its life into stamps[(block * NW + wave) * kStampCount + i].
+// XW (PW = 0, no merge): a wave takes the same units of every tile, so it
+// digitizes only its own units' x and starts its stream behind a wave barrier,
+// not a workgroup one; with the RMSNorm pre-op the waves' sums of squares meet
+// after the stream.  SKIPX (the Q4_0 RMSNorm launches at K = 4096): waves
+// holding no x item load nothing, where the plain instantiation's load the last
+// item again (measured: each form is the faster one for its own launches).
 constexpr int kStampCount = 8;
 template <int QT, int XQ, int NW, int D, int PW, int AMS, bool NTW, int TH, bool RP, bool ST = false, bool XW = false,
           bool SKIPX = false>
@@ -897,9 +903,10 @@ int launch_xq(const Planes& pw, const float* x, float* y, int M, int K, int grid
     return launch_rp<QT, XQ, NW, D, PW, AMS, NTW, TH, false>(pw, x, y, M, K, grid, lds, st, o);
 }
 
-// Q4_0, any K other than 4096 at 16 waves, no pre-op, every wave with a unit of
-// every tile: each wave digitizes only its own units' x (XW), with no
-// workgroup barrier before the stream.  Rounds of two units per wave.
+// Q4_0, any K other than 4096 at 16 waves, no pre-op or the RMSNorm, no
+// post-op, every wave with a unit of every tile and at most 4: each wave
+// digitizes only its own units' x (XW), with no workgroup barrier before the
+// stream.  Rounds of two units per wave.
 template <int NW, int D>
 int launch_xw(const Planes& pw, const float* x, float* y, int M, int K, int grid, size_t lds, hipStream_t st,
               const MatvecOpts& o) {
