@@ -386,13 +386,15 @@ def test_q4_kernels_edge_cases(hip, oracle, q4_kernel, kernel):
 
 
 @pytest.mark.parametrize("kernel", [native.Q4_KERNEL_MFMA], ids=["mfma"])
-def test_mfma_kernel_wide_dynamic_range_of_x(hip, oracle, q4_kernel, kernel):
+@pytest.mark.parametrize("K", [4096, 11008])
+def test_mfma_kernel_wide_dynamic_range_of_x(hip, oracle, q4_kernel, kernel, K):
     """x spanning up to 2^40 inside a block, with zero weights placed on the
     largest entries of some rows: the two-level fixed point keeps every row
-    within the bar."""
+    within the bar (K = 4096: x in registers; K = 11008: each wave digitizes its
+    own units' x)."""
     q4_kernel(kernel)
     rng = np.random.default_rng(90)
-    M, K = 256, 4096
+    M = 256
     blocks, _ = _weights(91, M, K)
     x = (rng.standard_normal(K) * 2.0 ** rng.integers(-20, 21, K)).astype(np.float32)
     big = np.argsort(-np.abs(x).reshape(-1, 32), axis=1)[:, 0] + 32 * np.arange(K // 32)
@@ -409,7 +411,8 @@ def test_mfma_kernel_wide_dynamic_range_of_x(hip, oracle, q4_kernel, kernel):
 @pytest.mark.parametrize("qt", ["q4", "q8"])
 @pytest.mark.parametrize("kernel", Q4_KERNELS, ids=Q4_KERNEL_IDS)
 @pytest.mark.parametrize("bad", ["nan", "inf", "-inf"])
-def test_non_finite_x_propagates(hip, oracle, q4_kernel, qt, kernel, bad):
+@pytest.mark.parametrize("K", [4096, 11008])
+def test_non_finite_x_propagates(hip, oracle, q4_kernel, qt, kernel, bad, K):
     """A NaN or infinite activation makes every row it touches non-finite, as
     in the reference's fp32 arithmetic: no kernel may turn it into a finite
     number.  Where the fp32 sum is +-inf (an infinite x times a nonzero weight)
@@ -418,7 +421,7 @@ def test_non_finite_x_propagates(hip, oracle, q4_kernel, qt, kernel, bad):
     infinity is not carried with its sign (a stated difference; the fp32 VALU
     kernel keeps the reference's +-inf)."""
     q4_kernel(kernel)
-    M, K = 300, 4096
+    M = 300
     blocks, x = _weights(44, M, K, qt)
     x[1234] = {"nan": np.nan, "inf": np.inf, "-inf": -np.inf}[bad]
     y = _gguf_matvec(hip, qt, blocks, x)
