@@ -614,8 +614,13 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
 
 }  // namespace
 
+// The single-workgroup kernels step an int index by up to 32768 (argmax) and
+// loop while it is below the length: lengths within that stride of INT32_MAX
+// would overflow the index and never end the loop.
+constexpr int64_t kMaxStridedLen = INT32_MAX - 65536;
+
 int rmsnorm_launch(const float* x, const float* w, float* y, int64_t dim, float eps, hipStream_t st) {
-    if (dim <= 0 || dim > INT32_MAX) return fail(kInvalidArgument, "rmsnorm: bad dim %lld", (long long)dim);
+    if (dim <= 0 || dim > kMaxStridedLen) return fail(kInvalidArgument, "rmsnorm: bad dim %lld", (long long)dim);
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, st, x, w, y, (int)dim, eps);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
@@ -644,7 +649,7 @@ int rope_kv_write_launch(float* qkv, void* k_cache, void* v_cache, int n_heads, 
 }
 
 int softmax_launch(const float* x, float* y, int64_t dim, hipStream_t st) {
-    if (dim <= 0 || dim > INT32_MAX) return fail(kInvalidArgument, "softmax: bad dim");
+    if (dim <= 0 || dim > kMaxStridedLen) return fail(kInvalidArgument, "softmax: bad dim");
     hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(1024), 0, st, x, y, (int)dim);
     ASMHIP_TRY(hipGetLastError());
     return kOk;
@@ -659,7 +664,7 @@ int swiglu_pairs_launch(const float* gu, float* h, int64_t H, hipStream_t st) {
 }
 
 int silu_launch(float* g, const float* u, int64_t dim, hipStream_t st) {
-    if (dim <= 0 || dim > INT32_MAX) return fail(kInvalidArgument, "silu_hadamard: bad dim");
+    if (dim <= 0 || dim > kMaxStridedLen) return fail(kInvalidArgument, "silu_hadamard: bad dim");
     hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((dim + kBlock - 1) / kBlock)), dim3(kBlock), 0, st, g, u,
                        (int)dim);
     ASMHIP_TRY(hipGetLastError());
@@ -669,6 +674,7 @@ int silu_launch(float* g, const float* u, int64_t dim, hipStream_t st) {
 int attention_launch(const float* q, const float* k, const float* v, float* y, int64_t seq, int64_t hd, float scale,
                      hipStream_t st) {
     if (seq <= 0 || hd <= 0) return fail(kInvalidArgument, "attention: need seq > 0 and head_dim > 0");
+    if (hd > kMaxStridedLen) return fail(kInvalidArgument, "attention: head_dim %lld", (long long)hd);
     if (seq > 40000) return fail(kUnsupported, "attention: seq_len %lld exceeds the LDS score buffer", (long long)seq);
     const int rc = dynamic_lds((const void*)attention_kernel, (size_t)seq * sizeof(float));
     if (rc) return rc;
@@ -799,6 +805,7 @@ int embed_launch(QuantType qt, const void* table, const int* token, float* x, in
 
 int argmax_launch(const float* logits, int n, int* token, int* pos, hipStream_t st, int* history, int history_len) {
     if (n <= 0) return fail(kInvalidArgument, "argmax: empty input");
+    if (n > kMaxStridedLen) return fail(kInvalidArgument, "argmax: %d logits", n);
     if (history && (!pos || history_len <= 0))
         return fail(kInvalidArgument, "argmax: a token history needs the position and a length");
     if (n % 4 == 0 && (uintptr_t)logits % 16 == 0)

@@ -121,3 +121,21 @@ def test_bench_trace_filters_name_built_kernels():
     assert bench.HEADLINE_KERNEL + "(" in names
     for fragment in ("gemm_q8_0_tiled<", "gemm_q8_0_coalesced<", "gemm_q8_split("):
         assert fragment in names, fragment
+
+
+def test_single_workgroup_ops_refuse_lengths_near_int_max():
+    """The one-workgroup decode ops step an int index by up to 32768 while it is
+    below the length; lengths that close to 2^31 are refused on the host before
+    anything is launched (the pointers below are never dereferenced)."""
+    lib = native.lib()
+    p, big = ctypes.c_void_p(256), 2 ** 31 - 1
+    calls = {
+        "rmsnorm": lambda: lib.asmhip_rmsnorm(p, p, p, big, 1e-6, None),
+        "softmax": lambda: lib.asmhip_softmax(p, p, big, None),
+        "silu_hadamard": lambda: lib.asmhip_silu_hadamard(p, p, big, None),
+        "attention": lambda: lib.asmhip_attention(p, p, p, p, 1, big, 1.0, None),
+        "argmax": lambda: lib.asmhip_argmax(p, big, p, None, None),
+    }
+    for name, call in calls.items():
+        assert call() == -1, name
+        assert name in native.last_error(), (name, native.last_error())
